@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FP8 quantized-linear path (one GPU).
+
+Workloads (synthetic data, seeded host generator luisaml_amd.synth):
+  * small-M decode linear (the headline line): x[M,4096] fp32 N(0,1) with
+    M in {1,4,16}, dynamically QuantizeLinear'd to E4M3 per tensor, times a
+    4096x11008 E4M3 weight (N(0,0.02), per-output-channel fp32 scales), bf16
+    out.  One step = the three linears, each = dynamic quantize kernel + GEMM
+    kernel.  Seven distinct copies of the packed weight (315 MB, more than the
+    256 MB MALL) are rotated so that every launch streams its weights from HBM.
+  * 8192^3 GEMM: A, B E4M3 quantised from N(0,1) with per-tensor scales
+    (amax/448), fp32 accumulate, bf16 out, fused scalar dequant scale.
+
+Prints ONE JSON line.  `value` is the small-M whole-step throughput (GB/s of
+algorithmic bytes with inputs resident in HBM); the 8192^3 GEMM TFLOP/s and
+both roofline fractions ride along in the same line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "FP8 GEMM TFLOPS (% of MFMA peak) at 8192³; small-M linear GB/s (% HBM peak)"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP8_PEAK_TFLOPS = 5000.0       # dense FP8 MFMA
+BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA (the exact kernel's instruction)
+SMALL_K, SMALL_N, SMALL_MS = 4096, 11008, (1, 4, 16)
+BIG = 8192
+N_WEIGHT_COPIES = 7
+
+
+def channel_scales_np(w: np.ndarray, axis: int) -> np.ndarray:
+    """Per-channel E4M3 scales amax/448 (1.0 when not a positive finite number)."""
+    amax = np.max(np.abs(np.nan_to_num(w, nan=0.0)), axis=axis).astype(np.float32)
+    s = (amax / np.float32(448.0)).astype(np.float32)
+    bad = ~(s > 0) | ~np.isfinite(s)
+    s[bad] = 1.0
+    return s
+
+
+def small_m_bytes(M: int) -> int:
+    """Algorithmic HBM bytes of one small-M linear (quantize + GEMM):
+    E4M3 weights + fp32 per-channel scales + fp32 activations in + bf16 out."""
+    return SMALL_K * SMALL_N + 4 * SMALL_N + 4 * M * SMALL_K + 2 * M * SMALL_N
+
+
+def gemm_kernel_bytes(M: int) -> int:
+    """Algorithmic bytes of the small-M GEMM kernel alone (E4M3 activations in)."""
+    return SMALL_K * SMALL_N + 4 * SMALL_N + M * SMALL_K + 2 * M * SMALL_N
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-big", action="store_true", help="skip the 8192^3 GEMM")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one plain 256 MiB device copy (profiler byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from luisaml_amd import capi, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3",
+           "data": "synthetic (seeded splitmix64 + Box-Muller, random-init weights)"}
+
+    # ------------------------------------------------------------ small-M --
+    K, N = SMALL_K, SMALL_N
+    w = synth.normal(101, (K, N), std=0.02)  # [K, N] (MatMul layout)
+    sw = channel_scales_np(w, axis=0)
+    d_sw = torch.from_numpy(sw).to(dev)
+    qw = capi.quantize(torch.from_numpy(w).to(dev), d_sw, axis=1)
+    packed = [capi.pack_weight(qw, w_is_nk=False)]
+    for _ in range(N_WEIGHT_COPIES - 1):
+        packed.append(packed[0].clone())
+    del qw
+    xs, qxs, sxs, ys = {}, {}, {}, {}
+    for M in SMALL_MS:
+        xs[M] = torch.from_numpy(synth.normal(200 + M, (M, K))).to(dev)
+        qxs[M] = torch.empty((M, K), dtype=torch.uint8, device=dev)
+        sxs[M] = torch.empty(1, dtype=torch.float32, device=dev)
+        ys[M] = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def linear(M, copy, evs=None):
+        if evs is not None:
+            evs[0].record(stream)
+        capi.quantize_dynamic(xs[M], out=qxs[M], scale_out=sxs[M], stream=stream)
+        if evs is not None:
+            evs[1].record(stream)
+        capi.gemm(qxs[M], sxs[M], packed[copy], d_sw, N, K, out=ys[M], kernel=capi.KERNEL_AUTO, stream=stream)
+        if evs is not None:
+            evs[2].record(stream)
+
+    def step(i, ev_list=None):
+        for j, M in enumerate(SMALL_MS):
+            linear(M, (3 * i + j) % N_WEIGHT_COPIES, None if ev_list is None else ev_list[j])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in SMALL_MS] for _ in range(args.steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t0.elapsed_time(t1) / args.steps
+    bytes_step = sum(small_m_bytes(M) for M in SMALL_MS)
+    value_gbs = bytes_step / (step_ms * 1e-3) / 1e9
+    gemm_ms = {M: float(np.mean([evs[i][j][1].elapsed_time(evs[i][j][2]) for i in range(args.steps)]))
+               for j, M in enumerate(SMALL_MS)}
+    quant_ms = {M: float(np.mean([evs[i][j][0].elapsed_time(evs[i][j][1]) for i in range(args.steps)]))
+                for j, M in enumerate(SMALL_MS)}
+    kbytes = sum(gemm_kernel_bytes(M) for M in SMALL_MS)
+    k_gbs = kbytes / (sum(gemm_ms.values()) * 1e-3) / 1e9
+    out.update({
+        "value": round(value_gbs, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 5),
+        "config": {"workload": "small-M FP8 linear: x[M,4096] fp32 -> dynamic per-tensor E4M3 -> "
+                               "x W[4096,11008] E4M3 (per-channel scales) -> bf16, M in {1,4,16}, "
+                               "one step = the three linears",
+                   "K": K, "N": N, "M": list(SMALL_MS), "weight_copies_rotated": N_WEIGHT_COPIES,
+                   "bytes_per_step": bytes_step, "pct_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 1)},
+        "roofline": {"bound": "hbm", "kernel": "k_gemm_skinny (exact bf16-MFMA instantiation)",
+                     "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "per_launch_bytes": {str(M): gemm_kernel_bytes(M) for M in SMALL_MS},
+                     "per_launch_us": {str(M): round(1e3 * gemm_ms[M], 2) for M in SMALL_MS},
+                     "quantize_us": {str(M): round(1e3 * quant_ms[M], 2) for M in SMALL_MS}},
+    })
+    del packed
+
+    # ------------------------------------------------------------ 8192^3 ---
+    if not args.no_big:
+        a = torch.from_numpy(synth.normal(301, (BIG, BIG))).to(dev)
+        b = torch.from_numpy(synth.normal(302, (BIG, BIG))).to(dev)  # [K, N]
+        qa, sa = capi.quantize_dynamic(a)
+        qb, sb = capi.quantize_dynamic(b)
+        del a, b
+        bp = capi.pack_weight(qb, w_is_nk=False)
+        del qb
+        y = torch.empty((BIG, BIG), dtype=torch.bfloat16, device=dev)
+        big = {}
+        for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
+                                 ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
+            for _ in range(max(1, args.warmup // 2)):
+                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern, stream=stream)
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            n = max(3, args.steps // 2)
+            e0.record(stream)
+            for _ in range(n):
+                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern, stream=stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / n
+            tflops = 2.0 * BIG ** 3 / (ms * 1e-3) / 1e12
+            big[name] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                         "pct_fp8_peak": round(100 * tflops / FP8_PEAK_TFLOPS, 1),
+                         "pct_instruction_peak": round(100 * tflops / peak, 1)}
+        out["gemm_8192"] = {"workload": "8192^3 E4M3 x E4M3, per-tensor scales, fp32 accumulate, bf16 out",
+                            "default_kernel": "exact_bf16_mfma", **big,
+                            "roofline": {"bound": "mfma", "achieved": big["exact_bf16_mfma"]["tflops"],
+                                         "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                         "frac": round(big["exact_bf16_mfma"]["tflops"] / FP8_PEAK_TFLOPS, 4)}}
+        del qa, bp, y
+
+    if args.calib_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = 256 << 20
+
+    # --------------------------------------------------------- CPU leg -----
+    if not args.no_cpu:
+        import oracle  # the CPU restatement of the reference arithmetic (baseline only)
+        nt = cpu_threads()
+        oracle.set_threads(nt)
+        wq = oracle.quantize(w, sw, axis=1)
+        t = time.perf_counter()
+        reps = 0
+        while True:
+            for M in SMALL_MS:
+                x = synth.normal(200 + M, (M, K))
+                s = oracle.dynamic_scale(x)
+                oracle.qlinear(oracle.quantize(x, s), s, wq, sw)
+            reps += 1
+            if time.perf_counter() - t > 8.0 or reps >= 5:
+                break
+        cpu_s = (time.perf_counter() - t) / reps
+        out["cpu_baseline"] = {"value": round(bytes_step / cpu_s / 1e9, 3), "unit": "GB/s", "cores": nt,
+                               "kind": "port",
+                               "sample": f"{reps} full steps of the small-M workload (M=1,4,16) through the "
+                                         "oracle: dynamic quantize, dequantize, fp32 fma-chain Gemm "
+                                         "(gemm.cpp:155-162 order), OpenMP over output tiles"}
+        if not args.no_big:
+            rows = 64
+            a = synth.normal(301, (BIG, BIG))[:rows]
+            b = synth.normal(302, (BIG, BIG))
+            qa_c = oracle.quantize(a, oracle.dynamic_scale(a))
+            sb_c = oracle.dynamic_scale(b)
+            qb_c = oracle.quantize(b, sb_c)
+            t = time.perf_counter()
+            oracle.qlinear(qa_c, 1.0, qb_c, sb_c)
+            dt = time.perf_counter() - t
+            out["cpu_baseline"]["gemm_8192_sample"] = {
+                "gflops": round(2.0 * rows * BIG * BIG / dt / 1e9, 2), "cores": nt,
+                "sample": f"{rows} rows of the 8192^3 GEMM (dequantize + fma-chain Gemm)"}
+
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

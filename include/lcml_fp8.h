@@ -1,0 +1,180 @@
+/*
+ * lcml_fp8.h -- C ABI of the MI355X (gfx950) FP8 quantized-linear library
+ * (liblcml_fp8.so).
+ *
+ * This is the drop-in boundary below the C++ operator registry
+ * (luisaml_amd/host): the reference ONNX runtime's Gemm / MatMul / Cast /
+ * QuantizeLinear / DequantizeLinear operators call into it.  Plain pointers
+ * and sizes only: every tensor argument is a DEVICE pointer, every `stream`
+ * is a hipStream_t passed as void* (NULL = the default stream).  Calls are
+ * asynchronous and stream-ordered; none synchronises the host.
+ *
+ * Status codes: 0 on success, negative on failure; the message of the last
+ * failure on the calling thread is returned by lcml_fp8_last_error().
+ *
+ * Data conventions
+ *   E4M3: OCP float8 E4M3FN, one byte per element, dense, row-major in ONNX
+ *         shape order (reference include/onnx/dynamic_array/fp8_data.h:25-43).
+ *   Encoder: the reference's saturating round-to-nearest-even
+ *         FP8E4M3FN::from_float (include/onnx/fp_quantized.h:149-223):
+ *         NaN -> 0x7f, +-0 -> 0x00, |x| > 448 or inf -> sign|0x7e,
+ *         otherwise RNE, underflow keeps the sign (0x80).
+ *   Decoder: FP8E4M3FN::to_float (fp_quantized.h:226-249); 0x7f/0xff = NaN.
+ *   Packed weights: see lcml_fp8_pack_weight.
+ */
+#ifndef LCML_FP8_H
+#define LCML_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define LCML_API __attribute__((visibility("default")))
+#else
+#define LCML_API
+#endif
+
+#define LCML_FP8_ABI_VERSION 1
+
+/* status codes */
+#define LCML_OK 0
+#define LCML_ERR_INVALID_ARG (-1)
+#define LCML_ERR_UNSUPPORTED (-2)
+#define LCML_ERR_HIP (-3)
+
+/* element type codes: the ONNX TensorProto.DataType numbers
+ * (reference include/onnx/onnx.h:31-60) */
+#define LCML_DTYPE_FLOAT 1
+#define LCML_DTYPE_BFLOAT16 16
+#define LCML_DTYPE_FLOAT8E4M3FN 17
+
+/* fused epilogue activations */
+#define LCML_ACT_NONE 0
+#define LCML_ACT_RELU 1      /* Relu, src/onnx/operators/unary.cpp:85 */
+#define LCML_ACT_GELU_ERF 2  /* Gelu approximate="none", gelu.cpp:122-126 */
+#define LCML_ACT_GELU_TANH 3 /* Gelu approximate="tanh", gelu.cpp:84-91 */
+
+/* kernel selection for the GEMM entry points.
+ * MFMA / SKINNY / VALU meet the reference tolerance (fp32-accurate
+ * accumulation; only the summation order differs).  The *_FP8 kernels run
+ * gfx950's native FP8 MFMAs at twice the matrix-core rate, but those
+ * instructions drop product bits more than ~2^13 below the largest product
+ * of each block (relative Frobenius error ~1.4e-5 on N(0,1) data, above the
+ * 1e-5 bar), so they are never picked by AUTO. */
+#define LCML_KERNEL_AUTO 0
+#define LCML_KERNEL_MFMA 1       /* 256x256 LDS double-buffered tiles, E4M3 widened to bf16 MFMA */
+#define LCML_KERNEL_SKINNY 2     /* small-M: weights streamed to registers, bf16 16x16x32 MFMA */
+#define LCML_KERNEL_VALU 3       /* small-M: 128-bit weight streaming, VALU fma, no MFMA */
+#define LCML_KERNEL_MFMA_FP8 4   /* as MFMA with v_mfma_f32_32x32x64_f8f6f4 */
+#define LCML_KERNEL_SKINNY_FP8 5 /* as SKINNY with v_mfma_f32_16x16x128_f8f6f4 */
+
+/* Message of the last failed call on this thread ("" if none). */
+LCML_API const char *lcml_fp8_last_error(void);
+
+/* LCML_FP8_ABI_VERSION of the loaded library. */
+LCML_API int lcml_fp8_abi_version(void);
+
+/*
+ * QuantizeLinear, float -> E4M3 (ONNX opset 21, saturate=1, zero point 0):
+ *   y[i] = from_float(x[i] / y_scale[a(i)])   (IEEE fp32 divide, bit-exact)
+ * The tensor is viewed as [outer, axis_len, inner]; y_scale holds axis_len
+ * entries (axis_len == 1: per-tensor scale).
+ * Replaces the reference's only float->fp8 conversion, Cast(to=FLOAT8E4M3FN)
+ * (src/onnx/operators/cast.cpp:63-67), and adds the QuantizeLinear op that
+ * its loader rejects (src/onnx/onnx.cpp:228-229).
+ */
+LCML_API int lcml_fp8_quantize(const float *x, uint8_t *y, int64_t outer, int64_t axis_len,
+                      int64_t inner, const float *y_scale, void *stream);
+
+/*
+ * DequantizeLinear, E4M3 -> float:  y[i] = to_float(x[i]) * x_scale[a(i)]
+ * (one fp32 multiply, bit-exact).  Same [outer, axis_len, inner] view.
+ * Replaces Cast(fp8 -> float) (cast.cpp:44-48) followed by Mul by the scale
+ * (src/onnx/operators/binary.cpp:347).
+ */
+LCML_API int lcml_fp8_dequantize(const uint8_t *x, float *y, int64_t outer, int64_t axis_len,
+                        int64_t inner, const float *x_scale, void *stream);
+
+/*
+ * Dynamic per-tensor quantisation:  amax = max |x| over non-NaN elements,
+ * scale = amax / 448 (1.0 when that is not a positive finite number),
+ * y = from_float(x / scale).  Writes the scale to *scale_out (device).
+ * workspace: device memory of LCML_FP8_DYNAMIC_WORKSPACE_BYTES; may be NULL
+ * when n <= LCML_FP8_DYNAMIC_SMALL_MAX (one-workgroup path).
+ * The reference has no dynamic quantiser; its nearest composition would be
+ * Abs -> ReduceMax (src/onnx/operators/reduce.cpp:417-459) -> Div -> Cast.
+ */
+#define LCML_FP8_DYNAMIC_WORKSPACE_BYTES 256
+#define LCML_FP8_DYNAMIC_SMALL_MAX 65536
+LCML_API int lcml_fp8_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
+                              void *workspace, void *stream);
+
+/* amax of x over non-NaN elements into *amax_out (device); 0 for n == 0. */
+LCML_API int lcml_fp8_amax(const float *x, int64_t n, float *amax_out, void *stream);
+
+/*
+ * Weight packing (load time).  The packed layout is "64-column panels of
+ * 16-byte k-chunks":  byte (k, n) of the logical [K, N] weight sits at
+ *     ((n / 64) * (Kp / 16) + k / 16) * 1024 + (n % 64) * 16 + k % 16
+ * with Kp = K rounded up to 128 and N rounded up to 64, padding zero-filled.
+ * Every 16-byte unit is one lane's operand chunk of a gfx950 FP8 MFMA
+ * (32x32x64 and 16x16x128), so a wavefront's fragment read is
+ * lane-contiguous and a column's k-run streams as 128-bit loads.
+ * w is [K, N] row-major (MatMul B) when w_is_nk == 0, or [N, K] row-major
+ * (Gemm transB=1, the torch Linear layout) when w_is_nk == 1.
+ * Replaces the dense FP8 weight binding of
+ * src/onnx/network_instance.cpp:215-232 (4-byte padded dense u8).
+ */
+LCML_API int64_t lcml_fp8_packed_weight_bytes(int64_t K, int64_t N);
+LCML_API int lcml_fp8_pack_weight(const uint8_t *w, int64_t K, int64_t N, int w_is_nk, uint8_t *packed,
+                         void *stream);
+LCML_API int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is_nk,
+                           uint8_t *w, void *stream);
+
+/*
+ * FP8 GEMM with fused epilogue (W8A8):
+ *   acc[m,n] = sum_k to_float(a[m,k]) * to_float(B[k,n])        (fp32)
+ *   y[m,n]   = act( alpha * acc * a_scale[0] * b_scale[n|0] + beta * C )
+ * a: E4M3 [M, K] row-major with row pitch lda bytes (lda % 16 == 0, a 16-byte
+ *    aligned; K % 16 == 0).
+ * b_packed: from lcml_fp8_pack_weight (K, N).
+ * b_scale: N entries if b_scale_per_channel, else 1.
+ * C (optional, may be NULL): fp32 with the reference Gemm broadcast rules
+ *    (gemm.cpp:81-103): c_ndim 0 or [1] -> scalar; 1-D of length N -> per
+ *    column, other 1-D -> per row; 2-D [c_dim0, c_dim1] with size-1 dims
+ *    broadcast.
+ * y: y_dtype LCML_DTYPE_FLOAT or LCML_DTYPE_BFLOAT16 (round to nearest
+ *    even), row pitch ldy elements.
+ * kernel: LCML_KERNEL_* (AUTO picks SKINNY for M <= 16, else MFMA).
+ * Replaces the per-thread fma loop nest of Gemm::apply (gemm.cpp:27-325) and
+ * MatMul (src/onnx/operators/mat_mul.cpp:51-186) for the DQ->Gemm pattern.
+ */
+LCML_API int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                  const float *a_scale, const uint8_t *b_packed, const float *b_scale,
+                  int b_scale_per_channel, float alpha, const float *c, int c_ndim,
+                  int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype,
+                  int64_t ldy, int kernel, void *stream);
+
+/*
+ * W8A32 linear: fp32 activations times packed E4M3 weights, same epilogue:
+ *   y[m,n] = act( alpha * (sum_k a[m,k] * to_float(B[k,n])) * b_scale[n|0]
+ *                 + beta * C )
+ * a: fp32 [M, K] row-major, row pitch lda elements (lda % 4 == 0).
+ * This is the reference graph DequantizeLinear(W) -> Gemm with unquantised
+ * activations (the 3-layer MLP).  Runs the VALU kernel (no MFMA).
+ */
+LCML_API int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda,
+                        const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel,
+                        float alpha, const float *c, int c_ndim, int64_t c_dim0,
+                        int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LCML_FP8_H */

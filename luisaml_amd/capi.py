@@ -1,0 +1,225 @@
+"""ctypes binding of the C ABI in include/lcml_fp8.h (liblcml_fp8.so).
+
+torch supplies device memory and the current HIP stream; every call goes
+straight to the gfx950 kernels of liblcml_fp8.so.  There is no fallback:
+if the library is missing or a call fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblcml_fp8.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "lcml_fp8.h")
+
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
+DTYPE_FLOAT, DTYPE_BFLOAT16, DTYPE_FLOAT8E4M3FN = 1, 16, 17
+ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_MFMA, KERNEL_SKINNY, KERNEL_VALU, KERNEL_MFMA_FP8, KERNEL_SKINNY_FP8 = 0, 1, 2, 3, 4, 5
+DYNAMIC_WORKSPACE_BYTES = 256
+DYNAMIC_SMALL_MAX = 65536
+PACK_K, PANEL_COLS = 128, 64
+
+
+class LcmlError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+_vp, _i64, _int, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
+_SIGS = {
+    "lcml_fp8_last_error": (C.c_char_p, []),
+    "lcml_fp8_abi_version": (_int, []),
+    "lcml_fp8_quantize": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "lcml_fp8_dequantize": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "lcml_fp8_quantize_dynamic": (_int, [_vp, _vp, _i64, _vp, _vp, _vp]),
+    "lcml_fp8_amax": (_int, [_vp, _i64, _vp, _vp]),
+    "lcml_fp8_packed_weight_bytes": (_i64, [_i64, _i64]),
+    "lcml_fp8_pack_weight": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
+    "lcml_fp8_unpack_weight": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
+    "lcml_fp8_gemm": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
+                             _i64, _i64, _f32, _int, _vp, _int, _i64, _int, _vp]),
+    "lcml_fp8_gemm_w8a32": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int,
+                                   _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
+}
+
+
+def header_symbols() -> list[str]:
+    """Every lcml_fp8_* function declared in include/lcml_fp8.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(lcml_fp8_\w+)\s*\(", text)))
+
+
+def lib():
+    """Load liblcml_fp8.so (built by luisaml_amd.build); raise if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m luisaml_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().lcml_fp8_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        raise LcmlError(rc, last_error())
+
+
+def _ptr(t: torch.Tensor | None):
+    if t is None:
+        return None
+    assert t.is_cuda, "device tensor expected"
+    return t.data_ptr()
+
+
+def _stream(stream=None):
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+
+
+# ----------------------------------------------------------- Q / DQ ---------
+
+def _axis_view(shape, axis, nscale):
+    n = 1
+    for s in shape:
+        n *= int(s)
+    if nscale == 1:
+        return 1, 1, n
+    axis = axis % len(shape)
+    outer = 1
+    for s in shape[:axis]:
+        outer *= int(s)
+    inner = 1
+    for s in shape[axis + 1:]:
+        inner *= int(s)
+    assert shape[axis] == nscale, "per-axis scale length must equal shape[axis]"
+    return outer, int(shape[axis]), inner
+
+
+def quantize(x: torch.Tensor, scale: torch.Tensor, axis: int = 1, out: torch.Tensor | None = None,
+             stream=None) -> torch.Tensor:
+    """QuantizeLinear fp32 -> E4M3 (uint8 tensor)."""
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    scale = scale.reshape(-1)
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    o, a, i = _axis_view(tuple(x.shape), axis, scale.numel())
+    _check(lib().lcml_fp8_quantize(_ptr(x), _ptr(y), o, a, i, _ptr(scale), _stream(stream)))
+    return y
+
+
+def dequantize(q: torch.Tensor, scale: torch.Tensor, axis: int = 1, out: torch.Tensor | None = None,
+               stream=None) -> torch.Tensor:
+    """DequantizeLinear E4M3 (uint8) -> fp32."""
+    assert q.dtype == torch.uint8 and q.is_contiguous()
+    scale = scale.reshape(-1)
+    y = out if out is not None else torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    o, a, i = _axis_view(tuple(q.shape), axis, scale.numel())
+    _check(lib().lcml_fp8_dequantize(_ptr(q), _ptr(y), o, a, i, _ptr(scale), _stream(stream)))
+    return y
+
+
+def quantize_dynamic(x: torch.Tensor, out: torch.Tensor | None = None,
+                     scale_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                     stream=None):
+    """Dynamic per-tensor quantisation; returns (codes, scale[1])."""
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    s = scale_out if scale_out is not None else torch.empty(1, dtype=torch.float32, device=x.device)
+    if workspace is None and x.numel() > DYNAMIC_SMALL_MAX:
+        workspace = torch.empty(DYNAMIC_WORKSPACE_BYTES, dtype=torch.uint8, device=x.device)
+    _check(lib().lcml_fp8_quantize_dynamic(_ptr(x), _ptr(y), x.numel(), _ptr(s), _ptr(workspace),
+                                           _stream(stream)))
+    return y, s
+
+
+def amax(x: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    o = out if out is not None else torch.empty(1, dtype=torch.float32, device=x.device)
+    _check(lib().lcml_fp8_amax(_ptr(x), x.numel(), _ptr(o), _stream(stream)))
+    return o
+
+
+# ------------------------------------------------------------ packing -------
+
+def packed_weight_bytes(K: int, N: int) -> int:
+    return int(lib().lcml_fp8_packed_weight_bytes(K, N))
+
+
+def pack_weight(w: torch.Tensor, w_is_nk: bool, stream=None) -> torch.Tensor:
+    """Pack an E4M3 weight ([K,N], or [N,K] when w_is_nk) into MFMA panels."""
+    assert w.dtype == torch.uint8 and w.is_contiguous() and w.dim() == 2
+    N, K = (w.shape[0], w.shape[1]) if w_is_nk else (w.shape[1], w.shape[0])
+    p = torch.empty(packed_weight_bytes(K, N), dtype=torch.uint8, device=w.device)
+    _check(lib().lcml_fp8_pack_weight(_ptr(w), K, N, int(w_is_nk), _ptr(p), _stream(stream)))
+    return p
+
+
+def unpack_weight(p: torch.Tensor, K: int, N: int, w_is_nk: bool, stream=None) -> torch.Tensor:
+    shape = (N, K) if w_is_nk else (K, N)
+    w = torch.empty(shape, dtype=torch.uint8, device=p.device)
+    _check(lib().lcml_fp8_unpack_weight(_ptr(p), K, N, int(w_is_nk), _ptr(w), _stream(stream)))
+    return w
+
+
+# --------------------------------------------------------------- GEMM -------
+
+_DTYPE_CODE = {torch.float32: DTYPE_FLOAT, torch.bfloat16: DTYPE_BFLOAT16, torch.float16: 10}
+
+
+def _c_args(c):
+    if c is None:
+        return None, 0, 0, 0
+    nd = c.dim()
+    return c, nd, (c.shape[0] if nd >= 1 else 0), (c.shape[1] if nd >= 2 else 0)
+
+
+def gemm(a: torch.Tensor, a_scale: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor,
+         N: int, K: int, c: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 1.0,
+         act: int = ACT_NONE, out_dtype=torch.float32, kernel: int = KERNEL_AUTO,
+         out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """W8A8 GEMM: a [M,K] E4M3 (uint8) x packed E4M3 weight -> [M,N] fp32/bf16."""
+    assert a.dtype == torch.uint8 and a.dim() == 2 and a.stride(1) == 1
+    M = a.shape[0]
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=a.device)
+    ydt = _DTYPE_CODE.get(y.dtype, 0)
+    cc, nd, c0, c1 = _c_args(c)
+    per_ch = int(b_scale.numel() > 1)
+    _check(lib().lcml_fp8_gemm(M, N, K, _ptr(a), a.stride(0), _ptr(a_scale), _ptr(b_packed),
+                               _ptr(b_scale), per_ch, float(alpha), _ptr(cc), nd, c0, c1,
+                               float(beta), int(act), _ptr(y), ydt, y.stride(0), int(kernel),
+                               _stream(stream)))
+    return y
+
+
+def gemm_w8a32(a: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor, N: int, K: int,
+               c: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 1.0,
+               act: int = ACT_NONE, out_dtype=torch.float32, out: torch.Tensor | None = None,
+               stream=None) -> torch.Tensor:
+    """W8A32 linear: a [M,K] fp32 x packed E4M3 weight -> [M,N]."""
+    assert a.dtype == torch.float32 and a.dim() == 2 and a.stride(1) == 1
+    M = a.shape[0]
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=a.device)
+    ydt = _DTYPE_CODE.get(y.dtype, 0)
+    cc, nd, c0, c1 = _c_args(c)
+    per_ch = int(b_scale.numel() > 1)
+    _check(lib().lcml_fp8_gemm_w8a32(M, N, K, _ptr(a), a.stride(0), _ptr(b_packed), _ptr(b_scale),
+                                     per_ch, float(alpha), _ptr(cc), nd, c0, c1, float(beta),
+                                     int(act), _ptr(y), ydt, y.stride(0), _stream(stream)))
+    return y

@@ -1,0 +1,206 @@
+// capi.hip -- the extern "C" boundary (include/lcml_fp8.h): argument
+// validation, kernel selection and error reporting.  No entry point
+// synchronises the host or allocates device memory.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/lcml_fp8.h"
+#include "lcml_internal.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t err, const char *what) {
+    if (err == hipSuccess) return LCML_OK;
+    return fail(LCML_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int check_view(int64_t outer, int64_t axis_len, int64_t inner, const char *fn) {
+    if (outer < 0 || axis_len < 1 || inner < 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: invalid view [outer=%lld, axis_len=%lld, inner=%lld]", fn,
+                    (long long)outer, (long long)axis_len, (long long)inner);
+    return LCML_OK;
+}
+
+// Shared validation of the GEMM epilogue arguments.
+int make_epilogue(lcml::Epilogue &e, const char *fn, int64_t M, int64_t N, const float *a_scale,
+                  const float *b_scale, int per_channel, float alpha, const float *c, int c_ndim,
+                  int64_t c0, int64_t c1, float beta, int act, void *y, int y_dtype, int64_t ldy) {
+    if (!b_scale) return fail(LCML_ERR_INVALID_ARG, "%s: b_scale is NULL", fn);
+    if (!y && M > 0 && N > 0) return fail(LCML_ERR_INVALID_ARG, "%s: y is NULL", fn);
+    if (y_dtype != LCML_DTYPE_FLOAT && y_dtype != LCML_DTYPE_BFLOAT16)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: output dtype %d (FLOAT=1 or BFLOAT16=16 supported)", fn, y_dtype);
+    if (ldy < N) return fail(LCML_ERR_INVALID_ARG, "%s: ldy=%lld < N=%lld", fn, (long long)ldy, (long long)N);
+    if (act < LCML_ACT_NONE || act > LCML_ACT_GELU_TANH)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: activation %d", fn, act);
+    const bool has_c = c != nullptr && beta != 0.0f;
+    if (has_c) {
+        if (c_ndim < 0 || c_ndim > 2) return fail(LCML_ERR_INVALID_ARG, "%s: C ndim %d", fn, c_ndim);
+        if (c_ndim == 1 && !(c0 == 1 || c0 == N || c0 == M))
+            return fail(LCML_ERR_INVALID_ARG, "%s: 1-D C of length %lld broadcasts to neither N nor M", fn,
+                        (long long)c0);
+        if (c_ndim == 2 && (!(c0 == 1 || c0 == M) || !(c1 == 1 || c1 == N)))
+            return fail(LCML_ERR_INVALID_ARG, "%s: C shape [%lld, %lld] does not broadcast to [%lld, %lld]",
+                        fn, (long long)c0, (long long)c1, (long long)M, (long long)N);
+    }
+    e.a_scale = a_scale;
+    e.b_scale = b_scale;
+    e.b_per_channel = per_channel ? 1 : 0;
+    e.alpha = alpha;
+    e.c = has_c ? c : nullptr;
+    e.c_ndim = c_ndim;
+    e.c0 = c0;
+    e.c1 = c1;
+    e.beta = beta;
+    e.act = act;
+    e.y = y;
+    e.y_bf16 = y_dtype == LCML_DTYPE_BFLOAT16;
+    e.ldy = ldy;
+    e.M = M;
+    e.N = N;
+    return LCML_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *lcml_fp8_last_error(void) { return g_err; }
+
+int lcml_fp8_abi_version(void) { return LCML_FP8_ABI_VERSION; }
+
+int lcml_fp8_quantize(const float *x, uint8_t *y, int64_t outer, int64_t axis_len, int64_t inner,
+                      const float *y_scale, void *stream) {
+    if (int rc = check_view(outer, axis_len, inner, "lcml_fp8_quantize")) return rc;
+    if (outer * axis_len * inner == 0) return LCML_OK;
+    if (!x || !y || !y_scale) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize: NULL pointer");
+    return hip_status(lcml::launch_quantize(x, y, outer, axis_len, inner, y_scale, (hipStream_t)stream),
+                      "lcml_fp8_quantize");
+}
+
+int lcml_fp8_dequantize(const uint8_t *x, float *y, int64_t outer, int64_t axis_len, int64_t inner,
+                        const float *x_scale, void *stream) {
+    if (int rc = check_view(outer, axis_len, inner, "lcml_fp8_dequantize")) return rc;
+    if (outer * axis_len * inner == 0) return LCML_OK;
+    if (!x || !y || !x_scale) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_dequantize: NULL pointer");
+    return hip_status(lcml::launch_dequantize(x, y, outer, axis_len, inner, x_scale, (hipStream_t)stream),
+                      "lcml_fp8_dequantize");
+}
+
+int lcml_fp8_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out, void *workspace,
+                              void *stream) {
+    if (n < 0) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize_dynamic: n < 0");
+    if (!scale_out) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize_dynamic: scale_out is NULL");
+    if (n > 0 && (!x || !y)) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize_dynamic: NULL pointer");
+    if (n > LCML_FP8_DYNAMIC_SMALL_MAX && !workspace)
+        return fail(LCML_ERR_INVALID_ARG,
+                    "lcml_fp8_quantize_dynamic: n=%lld needs a workspace of %d bytes", (long long)n,
+                    LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
+    return hip_status(lcml::launch_quantize_dynamic(x, y, n, scale_out, static_cast<uint32_t *>(workspace),
+                                                    (hipStream_t)stream),
+                      "lcml_fp8_quantize_dynamic");
+}
+
+int lcml_fp8_amax(const float *x, int64_t n, float *amax_out, void *stream) {
+    if (n < 0 || !amax_out || (n > 0 && !x)) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_amax: bad argument");
+    // The amax word is amax_out itself (fp32 bits of a non-negative float).
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t *word = reinterpret_cast<uint32_t *>(amax_out);
+    hipError_t err = lcml::launch_fill_u32(word, 0u, 1, s);
+    if (err == hipSuccess && n > 0) err = lcml::launch_amax(x, n, word, s);
+    return hip_status(err, "lcml_fp8_amax");
+}
+
+int64_t lcml_fp8_packed_weight_bytes(int64_t K, int64_t N) {
+    if (K <= 0 || N <= 0) return 0;
+    return lcml::pad_to(K, lcml::kPackK) * lcml::pad_to(N, lcml::kPanelCols);
+}
+
+int lcml_fp8_pack_weight(const uint8_t *w, int64_t K, int64_t N, int w_is_nk, uint8_t *packed,
+                         void *stream) {
+    if (K <= 0 || N <= 0 || !w || !packed)
+        return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_pack_weight: bad argument (K=%lld N=%lld)", (long long)K,
+                    (long long)N);
+    if (!aligned(packed, 16)) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_pack_weight: packed not 16-byte aligned");
+    return hip_status(lcml::launch_pack_weight(w, K, N, w_is_nk, packed, (hipStream_t)stream),
+                      "lcml_fp8_pack_weight");
+}
+
+int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is_nk, uint8_t *w,
+                           void *stream) {
+    if (K <= 0 || N <= 0 || !w || !packed)
+        return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_unpack_weight: bad argument");
+    if (!aligned(packed, 16)) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_unpack_weight: packed not 16-byte aligned");
+    return hip_status(lcml::launch_unpack_weight(packed, K, N, w_is_nk, w, (hipStream_t)stream),
+                      "lcml_fp8_unpack_weight");
+}
+
+int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda, const float *a_scale,
+                  const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
+                  const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
+                  int y_dtype, int64_t ldy, int kernel, void *stream) {
+    const char *fn = "lcml_fp8_gemm";
+    if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
+                                               (long long)M, (long long)N, (long long)K);
+    lcml::Epilogue e;
+    if (int rc = make_epilogue(e, fn, M, N, a_scale, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                               c_dim1, beta, act, y, y_dtype, ldy))
+        return rc;
+    if (M == 0) return LCML_OK;
+    if (!a || !b_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (K % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", fn, (long long)K);
+    if (lda < K || lda % 16 != 0 || !aligned(a, 16))
+        return fail(LCML_ERR_INVALID_ARG, "%s: a must be 16-byte aligned with lda >= K, lda %% 16 == 0", fn);
+    if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
+    hipStream_t s = (hipStream_t)stream;
+    if (kernel == LCML_KERNEL_AUTO) kernel = M <= 16 ? LCML_KERNEL_SKINNY : LCML_KERNEL_MFMA;
+    hipError_t err;
+    switch (kernel) {
+    case LCML_KERNEL_MFMA:
+    case LCML_KERNEL_MFMA_FP8:
+        // buffer offsets are 32-bit with 0x80000000 as the out-of-range marker
+        if ((M - 1) * lda + K >= (int64_t)0x80000000 || lcml_fp8_packed_weight_bytes(K, N) >= (int64_t)0x80000000)
+            return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the MFMA kernel", fn);
+        err = lcml::launch_gemm_mfma(M, N, K, a, lda, b_packed, e, kernel == LCML_KERNEL_MFMA, s);
+        break;
+    case LCML_KERNEL_SKINNY:
+    case LCML_KERNEL_SKINNY_FP8:
+        if (M > 16) return fail(LCML_ERR_UNSUPPORTED, "%s: the skinny kernel takes M <= 16 (M=%lld)", fn, (long long)M);
+        err = lcml::launch_gemm_skinny(M, N, K, a, lda, b_packed, e, kernel == LCML_KERNEL_SKINNY, s);
+        break;
+    case LCML_KERNEL_VALU: err = lcml::launch_gemv_valu_fp8(M, N, K, a, lda, b_packed, e, s); break;
+    default: return fail(LCML_ERR_INVALID_ARG, "%s: unknown kernel %d", fn, kernel);
+    }
+    return hip_status(err, fn);
+}
+
+int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, const uint8_t *b_packed,
+                        const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
+                        int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                        void *stream) {
+    const char *fn = "lcml_fp8_gemm_w8a32";
+    if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
+                                               (long long)M, (long long)N, (long long)K);
+    lcml::Epilogue e;
+    if (int rc = make_epilogue(e, fn, M, N, nullptr, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                               c_dim1, beta, act, y, y_dtype, ldy))
+        return rc;
+    if (M == 0) return LCML_OK;
+    if (!a || !b_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (lda < K || !aligned(a, 4)) return fail(LCML_ERR_INVALID_ARG, "%s: lda < K or a misaligned", fn);
+    if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
+    return hip_status(lcml::launch_gemv_valu_f32(M, N, K, a, lda, b_packed, e, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,262 @@
+// gemm_mfma.hip -- large-M FP8 GEMM on gfx950 matrix cores.
+//
+// Y[M,N] = epilogue( A[M,K] (E4M3, row-major) x B[K,N] (E4M3, packed panels) )
+//
+// Workgroup tile 256x256, K step 128, 512 threads = 8 wavefronts laid out
+// 2 (M) x 4 (N); each wavefront owns a 128x64 sub-tile = 4x2 blocks of
+// 32x32 fp32 accumulators (128 per lane).
+//
+// Two instantiations share everything but the matrix-core instruction:
+//   EXACT (default): the E4M3 fragments read from LDS are widened to bf16 in
+//     registers (v_cvt_scalef32_pk_bf16_fp8, exact) and multiplied with
+//     v_mfma_f32_32x32x16_bf16, which accumulates at fp32 accuracy.  Every
+//     product of two E4M3 values is exact in fp32, so the result differs from
+//     the fp32 reference only by summation order.
+//   FAST: v_mfma_f32_32x32x64_f8f6f4 directly on the E4M3 bytes.  Twice the
+//     matrix-core rate, but gfx950's FP8 MFMAs drop product bits more than
+//     about 2^13 below the largest product of each block (measured: relative
+//     Frobenius error ~1.4e-5 on N(0,1) data), so it is an opt-in kernel.
+// Two LDS stages of 64 KB (A 32 KB + B 32 KB).  Tiles move global -> LDS
+// with buffer_load_dwordx4 ... lds (no staging registers): each wavefront
+// instruction deposits one contiguous 1 KB block, lanes whose offset is out
+// of range (rows >= M, k >= K, panels beyond N) deposit zeros.  While the
+// matrix cores work on stage s the next K step streams into stage s^1; one
+// barrier per K step.
+//
+// LDS layouts (bank-conflict free for 16-lane groups of ds_read_b128 on the
+// 64-bank gfx950 LDS):
+//   A: row-major [256 rows][128 B]; the 16-byte chunk c of row r is stored
+//      at chunk position c ^ ((r >> 1) & 7).  A 1 KB load block is 8 rows;
+//      lane l fills position l%8 of row l/8, so it fetches logical chunk
+//      (l%8) ^ ((row >> 1) & 7) -- each 8-lane group still reads one
+//      contiguous 128 B row segment.
+//   B: the packed global layout verbatim, [4 panels][8 k-chunks][64 cols][16 B].
+// MFMA operand chunks: lane l of a 32x32x64 fragment holds row/column l%32
+// and k = (l/32)*32 + 0..31, i.e. two consecutive 16-byte k-chunks.
+//
+// Workgroup -> tile map: consecutive workgroup ids land on different XCDs
+// (id % 8), so ids are first regrouped so that each XCD works on one
+// contiguous range of tiles, and tiles are ordered in groups of 8 tile-rows
+// so that the tiles resident at one time on an XCD share A rows and B
+// columns in that XCD's L2.
+#include "lcml_internal.hpp"
+
+namespace lcml {
+namespace {
+
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int NT = 512;
+constexpr int A_BYTES = BM * BK;
+constexpr int B_BYTES = BN * BK;
+constexpr int STAGE = A_BYTES + B_BYTES;
+constexpr int EP_PITCH = 33;  // epilogue staging row pitch (floats)
+constexpr int LDS_BYTES = 2 * STAGE > 8 * 128 * EP_PITCH * 4 ? 2 * STAGE : 8 * 128 * EP_PITCH * 4;
+constexpr int GROUP_M = 8;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    int64_t M, N, K;
+    const uint8_t *a;
+    int64_t lda;
+    const uint8_t *bp;
+    int64_t KC;       // k-chunks per packed panel (Kp / 16)
+    int64_t npanels;  // packed panels (Np / 64)
+    uint32_t a_bytes, b_bytes;  // buffer extents for range checking
+    int tiles_m, tiles_n;
+    int nk;           // K steps of 128
+    Epilogue e;
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr uint32_t OOB = 0x80000000u;  // offset past every buffer extent
+
+__device__ inline v8i join(u4 lo, u4 hi) {
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+}
+
+__device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <bool EXACT>
+__global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+
+    // ---- tile selection -------------------------------------------------
+    const int ntiles = g.tiles_m * g.tiles_n;
+    int t = blockIdx.x;
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    const int per_group = GROUP_M * g.tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * GROUP_M;
+    const int gsize = min(g.tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (t % per_group) % gsize;
+    const int tn = (t % per_group) / gsize;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    // ---- global -> LDS block assignment ----------------------------------
+    // Wavefront w moves A blocks 4w..4w+3 (8 rows each) and B blocks
+    // 4w..4w+3 (panel b/8, k-chunk b%8) of every K step.
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, (int)g.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t b_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)g.bp, 0, (int)g.b_bytes, 0x00020000);
+    uint32_t a_off[4];
+    int a_kc[4];
+    uint32_t b_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (wave * 4 + i) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        a_kc[i] = c * 16;
+        a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
+        const int b = wave * 4 + i;
+        const int64_t panel = (n0 >> 6) + (b >> 3);
+        b_off[i] = panel < g.npanels ? (uint32_t)((panel * g.KC + (b & 7)) * 1024 + lane * 16) : OOB;
+    }
+    auto issue_tile = [&](int kt, int stage) {
+        uint8_t *sa = smem + stage * STAGE;
+        const uint32_t kbyte = (uint32_t)kt * BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t off =
+                (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * 4 + i) * 1024), 16,
+                                                     off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t off = b_off[i] != OOB ? b_off[i] + (uint32_t)kt * 8 * 1024 : OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                b_rsrc, (lds_void *)(sa + A_BYTES + (wave * 4 + i) * 1024), 16, off, 0, 0, 0);
+        }
+    };
+
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int kgrp = (lane >> 5) * 2;  // first k-chunk of this lane within a 64-k block
+    const int a_r0 = wm * 128 + (lane & 31);
+    const int b_col_off = wn * 8192 + (lane & 31) * 16;
+
+    issue_tile(0, 0);
+    __syncthreads();
+
+    for (int kt = 0; kt < g.nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < g.nk) issue_tile(kt + 1, cur ^ 1);
+        const uint8_t *sa = smem + cur * STAGE;
+        const uint8_t *sb = sa + A_BYTES;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int c0 = s * 4 + kgrp;
+            v8i bf[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint8_t *p = sb + b_col_off + j * 32 * 16 + c0 * 1024;
+                bf[j] = join(*reinterpret_cast<const u4 *>(p), *reinterpret_cast<const u4 *>(p + 1024));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = a_r0 + i * 32;
+                v8i af = join(*reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0)),
+                              *reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0 + 1)));
+                if constexpr (EXACT) {
+                    // 64 k of this lane's fragment = 4 groups of 8; group q feeds
+                    // the q-th 32x32x16 bf16 MFMA for both operands (the same k
+                    // permutation on A and B, so the dot product is unchanged).
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const bf16x8 a16 = e4m3x8_to_bf16((uint32_t)af[2 * q], (uint32_t)af[2 * q + 1]);
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                a16, e4m3x8_to_bf16((uint32_t)bf[j][2 * q], (uint32_t)bf[j][2 * q + 1]),
+                                acc[i][j], 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[i][j], 0, 0,
+                                                                                    0, 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue --------------------------------------------------------
+    // The accumulators go through LDS (free after the last barrier) one
+    // 32-column half of the wavefront tile at a time, so the epilogue runs as
+    // one rolled loop with a fixed column per lane instead of 128 unrolled
+    // copies of the activation code.  Row pitch 33 floats keeps the
+    // 2-row-per-instruction writes conflict free.
+    const Epilogue &e = g.e;
+    const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
+    float *st = reinterpret_cast<float *>(smem) + wave * (128 * EP_PITCH);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st[(i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EP_PITCH + (lane & 31)] = acc[i][j][r];
+        __syncthreads();
+        const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (col < e.N) {
+            const float sc = epi_scale(e, a_s, col);
+            const int64_t row0 = m0 + wm * 128 + (lane >> 5);
+#pragma unroll 1
+            for (int q = 0; q < 64; ++q) {
+                const int64_t row = row0 + 2 * q;
+                if (row >= e.M) break;
+                epi_store(e, row, col, epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
+            }
+        }
+        __syncthreads();
+    }
+}
+
+bool g_attr_set[2] = {false, false};
+
+}  // namespace
+
+hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
+    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_mfma<true>)
+                           : reinterpret_cast<const void *>(k_gemm_mfma<false>);
+    if (!g_attr_set[exact]) {
+        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+        if (err != hipSuccess) return err;
+        g_attr_set[exact] = true;
+    }
+    GemmArgs g;
+    g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
+    int64_t Kp = pad_to(K, kPackK), Np = pad_to(N, kPanelCols);
+    g.KC = Kp / 16;
+    g.npanels = Np / 64;
+    g.tiles_m = (int)((M + BM - 1) / BM);
+    g.tiles_n = (int)((N + BN - 1) / BN);
+    g.nk = (int)(Kp / BK);
+    g.a_bytes = (uint32_t)((M - 1) * lda + K);
+    g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
+    g.e = e;
+    if (exact)
+        hipLaunchKernelGGL(k_gemm_mfma<true>, dim3(g.tiles_m * g.tiles_n), dim3(NT), LDS_BYTES, s, g);
+    else
+        hipLaunchKernelGGL(k_gemm_mfma<false>, dim3(g.tiles_m * g.tiles_n), dim3(NT), LDS_BYTES, s, g);
+    return hipGetLastError();
+}
+
+}  // namespace lcml

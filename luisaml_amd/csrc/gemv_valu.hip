@@ -1,0 +1,163 @@
+// gemv_valu.hip -- small-M FP8-weight linear on the vector ALUs (no MFMA).
+//
+// Lane l of a wavefront owns output column (panel*64 + l).  In the packed
+// layout the 64 columns of a panel store each 16-byte k-chunk side by side,
+// so one 128-bit load per lane streams 1 KB of contiguous weights per
+// wavefront instruction.  The 16 weights are decoded with v_cvt_pk_f32_fp8
+// and folded into per-row fp32 fma chains; the activations are wave-uniform
+// and are read through the scalar data cache (constant address space), so
+// they occupy SGPR operands instead of VGPRs or LDS bandwidth.  A workgroup
+// of 4 wavefronts splits K four ways and sums the partial columns through
+// LDS (a cross-wavefront reduction; no cross-lane reduction is needed since
+// a lane owns its column).
+//
+// Activations are either fp32 (W8A32: DequantizeLinear(W) -> Gemm with
+// unquantised inputs) or E4M3 (W8A8, decoded per chunk).
+#include "lcml_internal.hpp"
+
+namespace lcml {
+namespace {
+
+constexpr int VW = 4;  // wavefronts per workgroup
+constexpr int VNT = VW * 64;
+constexpr int VMB = 4;  // rows per workgroup
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(4))) float cfloat;
+typedef const __attribute__((address_space(4))) uint32_t cu32;
+
+struct ValuArgs {
+    int64_t M, N, K;
+    const void *a;
+    int64_t lda;  // elements
+    const uint8_t *bp;
+    int64_t KC;
+    Epilogue e;
+};
+
+__device__ inline void decode16(u4 w, float *f) {
+    uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[q], false);
+        f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[q], true);
+        f[q * 4 + 0] = lo.x; f[q * 4 + 1] = lo.y; f[q * 4 + 2] = hi.x; f[q * 4 + 3] = hi.y;
+    }
+}
+
+// 16 uniform activation values of row m, k-chunk c (zero beyond K).
+template <bool FP8>
+__device__ inline void load_act16(const ValuArgs &g, int64_t m, int64_t c, float *a) {
+    const int64_t k0 = c * 16;
+    if (FP8) {
+        const uint8_t *row = static_cast<const uint8_t *>(g.a) + m * g.lda;
+        if (k0 + 16 <= g.K) {
+            cu32 *p = (cu32 *)(uintptr_t)(row + k0);
+            u4 w = {p[0], p[1], p[2], p[3]};
+            decode16(w, a);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                f2 v = __builtin_amdgcn_cvt_pk_f32_fp8(k0 + j < g.K ? (int)row[k0 + j] : 0, false);
+                a[j] = v.x;
+            }
+        }
+    } else {
+        const float *row = static_cast<const float *>(g.a) + m * g.lda;
+        if (k0 + 16 <= g.K) {
+            cfloat *p = (cfloat *)(uintptr_t)(row + k0);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a[j] = p[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a[j] = k0 + j < g.K ? row[k0 + j] : 0.0f;
+        }
+    }
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(VNT) void k_gemv_valu(ValuArgs g) {
+    __shared__ float red[VW][VMB][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t panel = blockIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.y * VMB;
+    const int rows = (int)min((int64_t)VMB, g.M - m0);
+    const int64_t c_begin = (g.KC * wave) / VW, c_end = (g.KC * (wave + 1)) / VW;
+    // chunks wholly beyond K hold zero weights; skip them
+    const int64_t c_live = (g.K + 15) / 16;
+    const int64_t c_stop = c_end < c_live ? c_end : c_live;
+
+    const uint8_t *wp = g.bp + panel * g.KC * 1024 + lane * 16;
+    float acc[VMB];
+#pragma unroll
+    for (int r = 0; r < VMB; ++r) acc[r] = 0.0f;
+
+    constexpr int U = 4;
+    for (int64_t c0 = c_begin; c0 < c_stop; c0 += U) {
+        u4 w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            w[u] = c0 + u < c_stop
+                       ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(wp + (c0 + u) * 1024))
+                       : u4{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u >= c_stop) break;
+            float wf[16];
+            decode16(w[u], wf);
+#pragma unroll
+            for (int r = 0; r < VMB; ++r) {
+                if (r >= rows) break;
+                float a[16];
+                load_act16<FP8>(g, m0 + r, c0 + u, a);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[r] = fmaf(a[j], wf[j], acc[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < VMB; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+
+    const Epilogue &e = g.e;
+    const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
+    const int64_t col = panel * 64 + lane;
+    // wave w finalises row w of the block
+    if (wave < rows && col < e.N) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < VW; ++w) v += red[w][wave][lane];
+        const int64_t row = m0 + wave;
+        epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
+    }
+}
+
+static_assert(VMB == VW, "one wavefront finalises one row");
+
+template <bool FP8>
+hipError_t launch_valu(int64_t M, int64_t N, int64_t K, const void *a, int64_t lda, const uint8_t *bp,
+                       const Epilogue &e, hipStream_t s) {
+    ValuArgs g;
+    g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
+    g.KC = pad_to(K, kPackK) / 16;
+    g.e = e;
+    int64_t npanels = pad_to(N, kPanelCols) / 64;
+    dim3 grid((unsigned)npanels, (unsigned)((M + VMB - 1) / VMB));
+    hipLaunchKernelGGL(k_gemv_valu<FP8>, grid, dim3(VNT), 0, s, g);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_valu_f32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda,
+                                const uint8_t *bp, const Epilogue &e, hipStream_t s) {
+    return launch_valu<false>(M, N, K, a, lda, bp, e, s);
+}
+
+hipError_t launch_gemv_valu_fp8(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                                const uint8_t *bp, const Epilogue &e, hipStream_t s) {
+    return launch_valu<true>(M, N, K, a, lda, bp, e, s);
+}
+
+}  // namespace lcml

@@ -1,0 +1,140 @@
+// lcml_device.hpp -- scalar helpers shared by the gfx950 kernels and the
+// host-side launch code: the E4M3 encoder, bf16 rounding, the epilogue
+// activations and the epilogue parameter block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lcml {
+
+__host__ __device__ inline uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ inline float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// fp32 -> E4M3FN with the reference encoder's exact behaviour
+// (FP8E4M3FN::from_float, include/onnx/fp_quantized.h:149-223):
+//   NaN -> 0x7f; +-0 -> 0x00; |x| > 448 or inf -> sign|0x7e;
+//   otherwise round to nearest even; a result of zero keeps the sign (0x80).
+// Written on the fp32 bit pattern (integer shifts, no frexp/floor), which is
+// the same rounding: the 24-bit significand is shifted right by 20 bits for
+// normal E4M3 results and by 141-e bits for subnormal ones, the remainder is
+// compared with the halfway point, and a carry out of the 3-bit mantissa
+// increments the exponent field through the integer add.
+__host__ __device__ inline uint32_t e4m3_encode(float x) {
+    uint32_t u = f32_bits(x);
+    uint32_t s = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7fu;      // NaN, sign ignored
+    if (a > 0x43e00000u) return s | 0x7eu;  // > 448 and inf saturate
+    if (a <= 0x3a800000u)                   // |x| <= 2^-10 rounds to zero
+        return a == 0 ? 0u : s;             // -0.0 -> 0x00, tiny -> signed 0
+    uint32_t e = a >> 23;                   // 117 .. 135
+    uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+    uint32_t shift = e >= 121u ? 20u : 141u - e;
+    uint32_t q = mant >> shift;
+    uint32_t rem = mant & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+    uint32_t code = e >= 121u ? ((e - 121u) << 3) + q : q;
+    if (code > 0x7eu) code = 0x7eu;
+    return code == 0 ? s : (s | code);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__host__ __device__ inline uint16_t bf16_rne(float f) {
+    uint32_t u = f32_bits(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Abramowitz & Stegun 7.1.26 erf, as in the reference
+// (include/onnx/operators/common.h:176-195).
+__device__ inline float as_erf(float x) {
+    float ax = fabsf(x);
+    float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float poly = t * (0.254829592f +
+                      t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+    float r = 1.0f - poly * expf(-ax * ax);
+    return x < 0.0f ? -r : r;
+}
+
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_ERF = 2, ACT_GELU_TANH = 3 };
+
+__device__ inline float apply_act(float v, int act) {
+    if (act == ACT_RELU) return v > 0.0f ? v : 0.0f;  // max(0, x), unary.cpp:85
+    if (act == ACT_GELU_ERF)                           // gelu.cpp:122-126
+        return v * 0.5f * (1.0f + as_erf(v * 0.70710678f));
+    if (act == ACT_GELU_TANH) {                        // gelu.cpp:84-91
+        float inner = 0.79788456f * fmaf(0.044715f * v * v, v, v);
+        return v * 0.5f * (1.0f + tanhf(inner));
+    }
+    return v;
+}
+
+// Epilogue of every GEMM kernel:
+//   y[m,n] = act(alpha * acc * a_scale * b_scale[n|0] + beta * C[bcast(m,n)])
+struct Epilogue {
+    const float *a_scale;  // device, 1 entry, or nullptr (= 1)
+    const float *b_scale;  // device, 1 or N entries
+    int b_per_channel;
+    float alpha;
+    const float *c;  // nullptr: no C
+    int c_ndim;
+    int64_t c0, c1;
+    float beta;
+    int act;
+    void *y;
+    int y_bf16;
+    int64_t ldy;
+    int64_t M, N;
+};
+
+// Bias under the reference Gemm broadcast rules (gemm.cpp:84-97).
+__device__ inline float epi_c(const Epilogue &e, int64_t m, int64_t n) {
+    if (e.c_ndim == 0 || (e.c_ndim == 1 && e.c0 == 1)) return e.c[0];
+    if (e.c_ndim == 1) return e.c0 == e.N ? e.c[n] : e.c[m];
+    int64_t ci = e.c0 == 1 ? 0 : m, cj = e.c1 == 1 ? 0 : n;
+    return e.c[ci * e.c1 + cj];
+}
+
+__device__ inline float epi_value(const Epilogue &e, float scale_n, int64_t m, int64_t n, float acc) {
+    float v = acc * scale_n;
+    if (e.alpha != 1.0f) v *= e.alpha;
+    if (e.c) v = e.beta == 1.0f ? v + epi_c(e, m, n) : v + e.beta * epi_c(e, m, n);
+    return apply_act(v, e.act);
+}
+
+// a_scale * b_scale[n] for column n.
+__device__ inline float epi_scale(const Epilogue &e, float a_s, int64_t n) {
+    float bs = e.b_per_channel ? e.b_scale[n] : e.b_scale[0];
+    return a_s * bs;
+}
+
+__device__ inline void epi_store(const Epilogue &e, int64_t m, int64_t n, float v) {
+    if (e.y_bf16)
+        reinterpret_cast<uint16_t *>(e.y)[m * e.ldy + n] = bf16_rne(v);
+    else
+        reinterpret_cast<float *>(e.y)[m * e.ldy + n] = v;
+}
+
+// E4M3 -> bf16 (exact: every E4M3 value is a bf16 value; 0x7f/0xff -> NaN)
+// for 8 consecutive bytes (two dwords) with v_cvt_scalef32_pk_bf16_fp8 at
+// scale 1.0, giving one 8-element operand of the bf16 MFMAs.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ inline bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
+    bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w0, 1.0f, false);
+    bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w0, 1.0f, true);
+    bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w1, 1.0f, false);
+    bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w1, 1.0f, true);
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Packed weight geometry (see lcml_fp8_pack_weight in include/lcml_fp8.h).
+__host__ __device__ inline int64_t pad_to(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+constexpr int kPanelCols = 64;   // columns per panel
+constexpr int kChunk = 16;       // bytes per k-chunk
+constexpr int kPackK = 128;      // K padding of packed weights
+
+}  // namespace lcml

@@ -1,0 +1,38 @@
+// lcml_internal.hpp -- launchers implemented in the .hip files and called by
+// the C ABI (capi.hip).  Each returns hipSuccess or the launch error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lcml_device.hpp"
+
+namespace lcml {
+
+hipError_t launch_quantize(const float *x, uint8_t *y, int64_t outer, int64_t axis_len,
+                           int64_t inner, const float *scale, hipStream_t s);
+hipError_t launch_dequantize(const uint8_t *x, float *y, int64_t outer, int64_t axis_len,
+                             int64_t inner, const float *scale, hipStream_t s);
+// amax into a zero-initialised uint word (atomic max on fp32 bits)
+hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream_t s);
+hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
+                                   uint32_t *work, hipStream_t s);
+hipError_t launch_amax_to_float(const uint32_t *amax_bits, float *out, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s);
+
+hipError_t launch_pack_weight(const uint8_t *w, int64_t K, int64_t N, int w_is_nk,
+                              uint8_t *packed, hipStream_t s);
+hipError_t launch_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is_nk,
+                                uint8_t *w, hipStream_t s);
+
+// exact: bf16 MFMAs on widened E4M3 (fp32-accurate); else native FP8 MFMAs
+hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
+hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                              const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
+hipError_t launch_gemv_valu_f32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda,
+                                const uint8_t *bp, const Epilogue &e, hipStream_t s);
+hipError_t launch_gemv_valu_fp8(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
+                                const uint8_t *bp, const Epilogue &e, hipStream_t s);
+
+}  // namespace lcml

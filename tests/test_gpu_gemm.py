@@ -1,0 +1,190 @@
+"""GPU parity of the FP8 GEMM kernels (MFMA tiles, skinny small-M, VALU
+small-M, W8A32) against the oracle's dequantise-then-Gemm composition
+(reference src/onnx/operators/gemm.cpp:27-325)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from luisaml_amd import capi
+from tests.gemm_cases import assert_close, make_case, reference
+
+pytestmark = pytest.mark.gpu
+
+KERNELS = {"mfma": capi.KERNEL_MFMA, "skinny": capi.KERNEL_SKINNY, "valu": capi.KERNEL_VALU,
+           "mfma_fp8": capi.KERNEL_MFMA_FP8, "skinny_fp8": capi.KERNEL_SKINNY_FP8}
+
+
+def run(c, kernel, bias=None, alpha=1.0, beta=1.0, act=capi.ACT_NONE, out_dtype=torch.float32, dev=None):
+    d_bias = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias, np.float32)).to(dev)
+    y = capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, c=d_bias, alpha=alpha, beta=beta, act=act,
+                  out_dtype=out_dtype, kernel=kernel)
+    return y
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 768, 1024), (300, 500, 784), (1, 64, 128),
+                                   (257, 100, 2304), (64, 10, 128), (1024, 1024, 4096)])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_mfma_shapes(dev, M, N, K, per_channel):
+    c = make_case(M, N, K, seed=M + N + K, per_channel=per_channel, dev=dev)
+    y = run(c, capi.KERNEL_MFMA, dev=dev).cpu().numpy()
+    ref, bound = reference(c)
+    assert_close(y, ref, bound)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 16])
+@pytest.mark.parametrize("N,K", [(64, 128), (11008, 4096), (100, 784), (4096, 11008)])
+@pytest.mark.parametrize("kernel", ["skinny", "valu"])
+def test_small_m_shapes(dev, M, N, K, kernel):
+    c = make_case(M, N, K, seed=M * 31 + N, dev=dev)
+    y = run(c, KERNELS[kernel], dev=dev).cpu().numpy()
+    ref, bound = reference(c)
+    assert_close(y, ref, bound)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("w_is_nk", [False, True])
+def test_weight_layouts(dev, kernel, w_is_nk):
+    M = 16 if kernel != "mfma" else 200
+    c = make_case(M, 320, 512, seed=5, w_is_nk=w_is_nk, dev=dev)
+    y = run(c, KERNELS[kernel], dev=dev).cpu().numpy()
+    ref, bound = reference(c)
+    assert_close(y, ref, bound)
+
+
+BIAS_SHAPES = ["N", "1", "scalar", "M1", "MN", "1N", "M"]
+
+
+def make_bias(kind, M, N, seed=1):
+    rng = np.random.default_rng(seed)
+    shape = {"N": (N,), "1": (1,), "scalar": (), "M1": (M, 1), "MN": (M, N), "1N": (1, N), "M": (M,)}[kind]
+    return (rng.standard_normal(shape) * 0.01).astype(np.float32)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("bias_kind", BIAS_SHAPES)
+def test_epilogue_bias_broadcast(dev, kernel, bias_kind):
+    M = 12 if kernel != "mfma" else 130
+    N = 192
+    c = make_case(M, N, 256, seed=7, dev=dev)
+    bias = make_bias(bias_kind, M, N)
+    y = run(c, KERNELS[kernel], bias=bias, alpha=0.75, beta=1.5, dev=dev).cpu().numpy()
+    ref, bound = reference(c, bias=bias, alpha=0.75, beta=1.5)
+    assert_close(y, ref, bound)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("act", [capi.ACT_RELU, capi.ACT_GELU_ERF, capi.ACT_GELU_TANH])
+def test_epilogue_activation(dev, kernel, act):
+    M = 16 if kernel != "mfma" else 256
+    c = make_case(M, 256, 512, seed=9, dev=dev)
+    bias = make_bias("N", M, 256, seed=3)
+    y = run(c, KERNELS[kernel], bias=bias, act=act, dev=dev).cpu().numpy()
+    ref, bound = reference(c, bias=bias, act=act)
+    assert_close(y, ref, bound, act=act)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("act", [capi.ACT_NONE, capi.ACT_GELU_ERF])
+def test_bf16_output_is_rne_of_fp32(dev, kernel, act):
+    """bf16 output is bit-exactly bf16_rne of the same kernel's fp32 output."""
+    M = 16 if kernel != "mfma" else 384
+    c = make_case(M, 448, 1024, seed=13, dev=dev)
+    bias = make_bias("N", M, 448, seed=4)
+    y32 = run(c, KERNELS[kernel], bias=bias, act=act, dev=dev).cpu().numpy()
+    y16 = run(c, KERNELS[kernel], bias=bias, act=act, out_dtype=torch.bfloat16, dev=dev)
+    got = y16.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.bf16_rne(y32))
+
+
+def test_kernels_agree_small_m(dev):
+    """All three kernels on one decode-shaped case agree within the bound."""
+    c = make_case(16, 2048, 4096, seed=21, dev=dev)
+    ref, bound = reference(c)
+    for k in ("mfma", "skinny", "valu"):
+        assert_close(run(c, KERNELS[k], dev=dev).cpu().numpy(), ref, bound)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 784), (64, 128, 256), (64, 10, 128), (1, 11008, 4096), (33, 70, 100)])
+def test_w8a32(dev, M, N, K):
+    from luisaml_amd import synth
+    a = synth.uniform(M * 5 + 1, (M, K))
+    w = synth.normal(M * 5 + 2, (N, K), std=0.05)
+    sw = np.array([oracle.dynamic_scale(w)], np.float32)
+    qw = oracle.quantize(w, sw)
+    bias = synth.normal(M * 5 + 3, (N,), std=0.01)
+    bp = capi.pack_weight(torch.from_numpy(qw).to(dev), True)
+    y = capi.gemm_w8a32(torch.from_numpy(a).to(dev), bp, torch.from_numpy(sw).to(dev), N, K,
+                        c=torch.from_numpy(bias).to(dev), act=capi.ACT_RELU).cpu().numpy()
+    B = oracle.dequantize(qw, sw)
+    ref = oracle.gemm(a, B, bias, transB=1, act=oracle.ACT_RELU)
+    bound = oracle.gemm_abs_bound(a, B, bias, transB=1)
+    assert_close(y, ref, bound)
+
+
+def test_nan_propagates(dev):
+    """A NaN code (0x7f) in A makes its output row NaN, in B its column."""
+    c = make_case(16, 128, 256, seed=2, dev=dev)
+    qa = c.qa.copy()
+    qa[3, 17] = 0x7F
+    qb = c.qb.copy()
+    qb[40, 77] = 0xFF  # [K, N]: column 77
+    c.d_qa = torch.from_numpy(qa).to(dev)
+    c.d_bp = capi.pack_weight(torch.from_numpy(qb).to(dev), False)
+    for k in ("mfma", "skinny", "valu"):
+        y = run(c, KERNELS[k], dev=dev).cpu().numpy()
+        assert np.isnan(y[3]).all(), k
+        assert np.isnan(y[:, 77]).all(), k
+        mask = np.ones_like(y, bool)
+        mask[3] = False
+        mask[:, 77] = False
+        assert not np.isnan(y[mask]).any(), k
+
+
+def test_errors_are_reported(dev):
+    c = make_case(8, 64, 128, seed=1, dev=dev)
+    with pytest.raises(capi.LcmlError) as e:
+        capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, out_dtype=torch.float16)
+    assert e.value.code == capi.ERR_UNSUPPORTED
+    big = make_case(17, 64, 128, seed=1, dev=dev)
+    with pytest.raises(capi.LcmlError) as e:
+        capi.gemm(big.d_qa, big.d_sa, big.d_bp, big.d_sb, big.N, big.K, kernel=capi.KERNEL_SKINNY)
+    assert e.value.code == capi.ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_fp8", "skinny_fp8"])
+def test_identity_reproduces_every_code(dev, kernel):
+    """One-hot A rows (1.0 = 0x38) pick single weights: y[m, n] = to_float(B[m, n])
+    exactly, for all 254 non-NaN E4M3 codes, through each kernel's operand
+    conversion.  (NaN codes are left out: 0 * NaN from the other rows would
+    poison the column; NaN propagation has its own test.)  Zeros compare by
+    value: -0.0 + 0 * b sums to +0.0."""
+    M = 16 if "skinny" in kernel or kernel == "valu" else 128
+    K, N = 128, 256
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    qa = np.zeros((M, K), np.uint8)
+    qa[np.arange(M), np.arange(M)] = 0x38
+    rng = np.random.default_rng(0)
+    qb = np.zeros((K, N), np.uint8)
+    for k in range(M):
+        qb[k, :254] = rng.permutation(codes)
+    one = torch.ones(1, device=dev)
+    bp = capi.pack_weight(torch.from_numpy(qb).to(dev), False)
+    y = capi.gemm(torch.from_numpy(qa).to(dev), one, bp, one, N, K, kernel=KERNELS[kernel]).cpu().numpy()
+    ref = oracle.e4m3_to_float(qb[:M])
+    assert np.array_equal(y, ref)
+    nz = ref != 0
+    assert np.array_equal(y[nz].view(np.uint32), ref[nz].view(np.uint32))
+
+
+@pytest.mark.parametrize("kernel", ["mfma_fp8", "skinny_fp8"])
+def test_native_fp8_mfma_precision_is_documented(dev, kernel):
+    """The opt-in native-FP8-MFMA kernels stay inside the elementwise bound and
+    within 3e-5 relative Frobenius (gfx950 FP8 MFMA block truncation)."""
+    M = 16 if "skinny" in kernel else 512
+    c = make_case(M, 1024, 4096, seed=17, dev=dev)
+    y = run(c, KERNELS[kernel], dev=dev).cpu().numpy().astype(np.float64)
+    ref, bound = reference(c)
+    assert np.all(np.abs(y - ref) <= 1e-4 * bound)
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert rel < 3e-5
