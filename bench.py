@@ -104,56 +104,80 @@ def main() -> int:
         sxs[M] = torch.empty(1, dtype=torch.float32, device=dev)
         ys[M] = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
-    def linear(M, copy, evs=None):
-        if evs is not None:
-            evs[0].record(stream)
-        capi.quantize_dynamic(xs[M], out=qxs[M], scale_out=sxs[M], stream=stream)
-        if evs is not None:
-            evs[1].record(stream)
-        capi.gemm(qxs[M], sxs[M], packed[copy], d_sw, N, K, out=ys[M], kernel=capi.KERNEL_AUTO, stream=stream)
-        if evs is not None:
-            evs[2].record(stream)
+    def linear(M, copy, gemm_only=False):
+        if not gemm_only:
+            capi.quantize_dynamic(xs[M], out=qxs[M], scale_out=sxs[M])
+        capi.gemm(qxs[M], sxs[M], packed[copy], d_sw, N, K, out=ys[M], kernel=capi.KERNEL_AUTO)
 
-    def step(i, ev_list=None):
+    def step(i, gemm_only=False):
         for j, M in enumerate(SMALL_MS):
-            linear(M, (3 * i + j) % N_WEIGHT_COPIES, None if ev_list is None else ev_list[j])
+            linear(M, (3 * i + j) % N_WEIGHT_COPIES, gemm_only)
 
+    def capture(fn, n):
+        """HIP graph of n calls of fn(i) on a side stream (kernels only, no memsets)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(2):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        torch.cuda.synchronize()
+        return g
+
+    def timed(fn):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    # eager warmup, then the timed region: one replay of a graph holding
+    # exactly `steps` steps (launch gaps of the Python/ctypes caller removed)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in SMALL_MS] for _ in range(args.steps)]
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i, evs[i])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    step_ms = t0.elapsed_time(t1) / args.steps
+    g_steps = capture(step, args.steps)
+    g_steps.replay()
+    step_ms = timed(g_steps.replay) / args.steps
+    eager_ms = timed(lambda: [step(i) for i in range(args.steps)]) / args.steps
+    # the GEMM kernel alone, same weight rotation: its average launch duration
+    g_gemm = capture(lambda i: step(i, gemm_only=True), args.steps)
+    g_gemm.replay()
+    gemm_ms_total = timed(g_gemm.replay) / args.steps  # three GEMM launches per step
     bytes_step = sum(small_m_bytes(M) for M in SMALL_MS)
     value_gbs = bytes_step / (step_ms * 1e-3) / 1e9
-    gemm_ms = {M: float(np.mean([evs[i][j][1].elapsed_time(evs[i][j][2]) for i in range(args.steps)]))
-               for j, M in enumerate(SMALL_MS)}
-    quant_ms = {M: float(np.mean([evs[i][j][0].elapsed_time(evs[i][j][1]) for i in range(args.steps)]))
-                for j, M in enumerate(SMALL_MS)}
     kbytes = sum(gemm_kernel_bytes(M) for M in SMALL_MS)
-    k_gbs = kbytes / (sum(gemm_ms.values()) * 1e-3) / 1e9
+    k_gbs = kbytes / (gemm_ms_total * 1e-3) / 1e9
+    per_launch = {}
+    for M in SMALL_MS:
+        gm = capture(lambda i, M=M: linear(M, i % N_WEIGHT_COPIES, gemm_only=True), 3 * args.steps)
+        gm.replay()
+        per_launch[str(M)] = round(1e3 * timed(gm.replay) / (3 * args.steps), 2)
+        del gm
     out.update({
         "value": round(value_gbs, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 5),
+        "ms_per_step_eager_launches": round(eager_ms, 5),
         "config": {"workload": "small-M FP8 linear: x[M,4096] fp32 -> dynamic per-tensor E4M3 -> "
                                "x W[4096,11008] E4M3 (per-channel scales) -> bf16, M in {1,4,16}, "
-                               "one step = the three linears",
+                               "one step = the three linears (6 kernels), timed as one HIP-graph replay",
                    "K": K, "N": N, "M": list(SMALL_MS), "weight_copies_rotated": N_WEIGHT_COPIES,
                    "bytes_per_step": bytes_step, "pct_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm", "kernel": "k_gemm_skinny (exact bf16-MFMA instantiation)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "per_launch_bytes": {str(M): gemm_kernel_bytes(M) for M in SMALL_MS},
-                     "per_launch_us": {str(M): round(1e3 * gemm_ms[M], 2) for M in SMALL_MS},
-                     "quantize_us": {str(M): round(1e3 * quant_ms[M], 2) for M in SMALL_MS}},
+                     "bytes_per_launch": {str(M): gemm_kernel_bytes(M) for M in SMALL_MS},
+                     "avg_launch_us": {str(M): per_launch[str(M)] for M in SMALL_MS},
+                     "avg_launch_us_all": round(1e3 * gemm_ms_total / 3, 2)},
     })
-    del packed
+    del g_steps, g_gemm
 
     # ------------------------------------------------------------ 8192^3 ---
     if not args.no_big:
@@ -169,17 +193,9 @@ def main() -> int:
         for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
                                  ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
             for _ in range(max(1, args.warmup // 2)):
-                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern, stream=stream)
-            torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
+                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern)
             n = max(3, args.steps // 2)
-            e0.record(stream)
-            for _ in range(n):
-                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern, stream=stream)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / n
+            ms = timed(lambda: [capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern) for _ in range(n)]) / n
             tflops = 2.0 * BIG ** 3 / (ms * 1e-3) / 1e12
             big[name] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
                          "pct_fp8_peak": round(100 * tflops / FP8_PEAK_TFLOPS, 1),

@@ -173,6 +173,26 @@ LCML_API int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a
                         int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
                         void *stream);
 
+/*
+ * Plain fp32 Gemm for graphs that stay in fp32 (no FP8 pattern to fuse):
+ * Y = act(alpha * op(A) op(B) + beta * C), op = transpose when trans_*;
+ * every output is one sequential fma chain over k from 0, exactly the
+ * reference's scalar Gemm order (src/onnx/operators/gemm.cpp:155-162).
+ * a: [M,K] (or [K,M] when trans_a) with row pitch lda; b: [K,N] (or [N,K]
+ * when trans_b) with row pitch ldb; C and y as in lcml_fp8_gemm.
+ */
+LCML_API int lcml_fp8_sgemm(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, int trans_a,
+                            const float *b, int64_t ldb, int trans_b, float alpha, const float *c, int c_ndim,
+                            int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype,
+                            int64_t ldy, void *stream);
+
+/*
+ * Elementwise fp32 activation y = act(x) for an unfused Relu
+ * (src/onnx/operators/unary.cpp:85) or Gelu (src/onnx/operators/gelu.cpp:
+ * 84-91, 122-126); act is LCML_ACT_*.  y may equal x.
+ */
+LCML_API int lcml_fp8_activation(const float *x, float *y, int64_t n, int act, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

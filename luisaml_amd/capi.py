@@ -48,6 +48,9 @@ _SIGS = {
                              _i64, _i64, _f32, _int, _vp, _int, _i64, _int, _vp]),
     "lcml_fp8_gemm_w8a32": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int,
                                    _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
+    "lcml_fp8_sgemm": (_int, [_i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _f32, _vp, _int, _i64,
+                              _i64, _f32, _int, _vp, _int, _i64, _vp]),
+    "lcml_fp8_activation": (_int, [_vp, _vp, _i64, _int, _vp]),
 }
 
 
@@ -222,4 +225,25 @@ def gemm_w8a32(a: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor, N
     _check(lib().lcml_fp8_gemm_w8a32(M, N, K, _ptr(a), a.stride(0), _ptr(b_packed), _ptr(b_scale),
                                      per_ch, float(alpha), _ptr(cc), nd, c0, c1, float(beta),
                                      int(act), _ptr(y), ydt, y.stride(0), _stream(stream)))
+    return y
+
+
+def sgemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 1.0,
+          trans_a: bool = False, trans_b: bool = False, act: int = ACT_NONE, stream=None) -> torch.Tensor:
+    """Plain fp32 Gemm in the reference's per-output fma-chain order."""
+    assert a.dtype == torch.float32 and b.dtype == torch.float32 and a.is_contiguous() and b.is_contiguous()
+    M, K = (a.shape[1], a.shape[0]) if trans_a else (a.shape[0], a.shape[1])
+    N = b.shape[0] if trans_b else b.shape[1]
+    y = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    cc, nd, c0, c1 = _c_args(c)
+    _check(lib().lcml_fp8_sgemm(M, N, K, _ptr(a), a.shape[1], int(trans_a), _ptr(b), b.shape[1], int(trans_b),
+                                float(alpha), _ptr(cc), nd, c0, c1, float(beta), int(act), _ptr(y), DTYPE_FLOAT,
+                                N, _stream(stream)))
+    return y
+
+
+def activation(x: torch.Tensor, act: int, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    y = out if out is not None else torch.empty_like(x)
+    _check(lib().lcml_fp8_activation(_ptr(x), _ptr(y), x.numel(), int(act), _stream(stream)))
     return y

@@ -36,8 +36,9 @@ int check_view(int64_t outer, int64_t axis_len, int64_t inner, const char *fn) {
 // Shared validation of the GEMM epilogue arguments.
 int make_epilogue(lcml::Epilogue &e, const char *fn, int64_t M, int64_t N, const float *a_scale,
                   const float *b_scale, int per_channel, float alpha, const float *c, int c_ndim,
-                  int64_t c0, int64_t c1, float beta, int act, void *y, int y_dtype, int64_t ldy) {
-    if (!b_scale) return fail(LCML_ERR_INVALID_ARG, "%s: b_scale is NULL", fn);
+                  int64_t c0, int64_t c1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                  bool scales_optional = false) {
+    if (!b_scale && !scales_optional) return fail(LCML_ERR_INVALID_ARG, "%s: b_scale is NULL", fn);
     if (!y && M > 0 && N > 0) return fail(LCML_ERR_INVALID_ARG, "%s: y is NULL", fn);
     if (y_dtype != LCML_DTYPE_FLOAT && y_dtype != LCML_DTYPE_BFLOAT16)
         return fail(LCML_ERR_UNSUPPORTED, "%s: output dtype %d (FLOAT=1 or BFLOAT16=16 supported)", fn, y_dtype);
@@ -201,6 +202,31 @@ int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t
     if (lda < K || !aligned(a, 4)) return fail(LCML_ERR_INVALID_ARG, "%s: lda < K or a misaligned", fn);
     if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
     return hip_status(lcml::launch_gemv_valu_f32(M, N, K, a, lda, b_packed, e, (hipStream_t)stream), fn);
+}
+
+int lcml_fp8_sgemm(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, int trans_a, const float *b,
+                   int64_t ldb, int trans_b, float alpha, const float *c, int c_ndim, int64_t c_dim0,
+                   int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy, void *stream) {
+    const char *fn = "lcml_fp8_sgemm";
+    if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
+                                               (long long)M, (long long)N, (long long)K);
+    lcml::Epilogue e;
+    if (int rc = make_epilogue(e, fn, M, N, nullptr, nullptr, 0, alpha, c, c_ndim, c_dim0, c_dim1, beta, act, y,
+                               y_dtype, ldy, true))
+        return rc;
+    if (M == 0) return LCML_OK;
+    if (!a || !b) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N))
+        return fail(LCML_ERR_INVALID_ARG, "%s: leading dimension too small", fn);
+    return hip_status(lcml::launch_sgemm(M, N, K, a, lda, trans_a, b, ldb, trans_b, e, (hipStream_t)stream), fn);
+}
+
+int lcml_fp8_activation(const float *x, float *y, int64_t n, int act, void *stream) {
+    if (n < 0 || act < LCML_ACT_NONE || act > LCML_ACT_GELU_TANH)
+        return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_activation: n=%lld act=%d", (long long)n, act);
+    if (n == 0) return LCML_OK;
+    if (!x || !y) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_activation: NULL pointer");
+    return hip_status(lcml::launch_activation(x, y, n, act, (hipStream_t)stream), "lcml_fp8_activation");
 }
 
 }  // extern "C"

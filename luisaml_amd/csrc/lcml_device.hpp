@@ -76,7 +76,7 @@ __device__ inline float apply_act(float v, int act) {
 //   y[m,n] = act(alpha * acc * a_scale * b_scale[n|0] + beta * C[bcast(m,n)])
 struct Epilogue {
     const float *a_scale;  // device, 1 entry, or nullptr (= 1)
-    const float *b_scale;  // device, 1 or N entries
+    const float *b_scale;  // device, 1 or N entries, or nullptr (= 1)
     int b_per_channel;
     float alpha;
     const float *c;  // nullptr: no C
@@ -107,7 +107,7 @@ __device__ inline float epi_value(const Epilogue &e, float scale_n, int64_t m, i
 
 // a_scale * b_scale[n] for column n.
 __device__ inline float epi_scale(const Epilogue &e, float a_s, int64_t n) {
-    float bs = e.b_per_channel ? e.b_scale[n] : e.b_scale[0];
+    float bs = e.b_scale ? (e.b_per_channel ? e.b_scale[n] : e.b_scale[0]) : 1.0f;
     return a_s * bs;
 }
 

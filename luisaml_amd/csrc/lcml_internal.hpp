@@ -35,4 +35,8 @@ hipError_t launch_gemv_valu_f32(int64_t M, int64_t N, int64_t K, const float *a,
 hipError_t launch_gemv_valu_fp8(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                                 const uint8_t *bp, const Epilogue &e, hipStream_t s);
 
+hipError_t launch_sgemm(int64_t M, int64_t N, int64_t K, const float *A, int64_t lda, int transA, const float *B,
+                        int64_t ldb, int transB, const Epilogue &e, hipStream_t s);
+hipError_t launch_activation(const float *x, float *y, int64_t n, int act, hipStream_t s);
+
 }  // namespace lcml

@@ -136,24 +136,38 @@ __device__ inline float block_max(float m, float *red) {
     return m;
 }
 
-// amax: each block reduces its grid-stride share, then one atomic max on the
-// fp32 bits (non-negative floats order like their unsigned bit patterns).
-__global__ __launch_bounds__(kThreads) void k_amax(const float *__restrict__ x, int64_t n,
-                                                   uint32_t *__restrict__ amax_bits) {
-    __shared__ float red[kThreads / 64];
+// amax: each block reduces its grid-stride share (8 float4 loads in flight
+// per thread), then one atomic max on the fp32 bits (non-negative floats
+// order like their unsigned bit patterns).  The grid is capped at 256
+// workgroups so the same-address atomics stay few.
+constexpr int kAmaxThreads = 512;
+constexpr int kAmaxU = 8;
+
+__global__ __launch_bounds__(kAmaxThreads) void k_amax(const float *__restrict__ x, int64_t n,
+                                                       uint32_t *__restrict__ amax_bits) {
+    __shared__ float red[kAmaxThreads / 64];
     float m = 0.0f;
     bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t nv = vec ? n / 4 : 0;
+    const int64_t nv = vec ? n / 4 : 0;
     const f4 *x4 = reinterpret_cast<const f4 *>(x);
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nv; i += stride) {
-        f4 v = __builtin_nontemporal_load(x4 + i);
-        m = absmax_acc(m, v.x); m = absmax_acc(m, v.y);
-        m = absmax_acc(m, v.z); m = absmax_acc(m, v.w);
+    const int64_t stride = (int64_t)gridDim.x * kAmaxThreads * kAmaxU;
+    for (int64_t i0 = (int64_t)blockIdx.x * kAmaxThreads * kAmaxU + threadIdx.x; i0 < nv; i0 += stride) {
+        f4 v[kAmaxU];
+#pragma unroll
+        for (int u = 0; u < kAmaxU; ++u) {
+            const int64_t i = i0 + (int64_t)u * kAmaxThreads;
+            v[u] = i < nv ? __builtin_nontemporal_load(x4 + i) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < kAmaxU; ++u) {
+            m = absmax_acc(m, v[u].x); m = absmax_acc(m, v[u].y);
+            m = absmax_acc(m, v[u].z); m = absmax_acc(m, v[u].w);
+        }
     }
-    for (int64_t i = nv * 4 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+    for (int64_t i = nv * 4 + (int64_t)blockIdx.x * kAmaxThreads + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kAmaxThreads)
         m = absmax_acc(m, x[i]);
-    m = block_max<kThreads>(m, red);
+    m = block_max<kAmaxThreads>(m, red);
     if (threadIdx.x == 0) atomicMax(amax_bits, f32_bits(m));
 }
 
@@ -170,11 +184,45 @@ __global__ void k_amax_to_float(const uint32_t *amax_bits, float *out) {
     if (threadIdx.x == 0) *out = bits_f32(*amax_bits);
 }
 
-// Whole dynamic quantisation of a small tensor in one workgroup: an amax
-// pass, then an encode pass that re-reads x (it is in L2 by then).
+// Dynamic quantisation of a small tensor in ONE launch with no workspace:
+// each of the P workgroups reduces the amax of the whole tensor (float4
+// loads, L2-resident after the first workgroup touches it), then encodes
+// only its own 1/P slice, so the IEEE divide + encode work (~30 VALU ops per
+// element) is spread over P CUs instead of one.
 constexpr int kSmallThreads = 1024;
 constexpr int64_t kSmallMax = 65536;
+constexpr int kRedThreads = 1024;
 
+__global__ __launch_bounds__(kRedThreads) void k_quantize_dynamic_spread(
+    const float *__restrict__ x, uint8_t *__restrict__ y, int64_t n4, float *__restrict__ scale_out) {
+    __shared__ float red[kRedThreads / 64];
+    const f4 *x4 = reinterpret_cast<const f4 *>(x);
+    float m = 0.0f;
+    constexpr int U = 16;  // 1024 threads x 16 float4 = the whole 64K-element tensor in one round trip
+    for (int64_t i0 = threadIdx.x; i0 < n4; i0 += (int64_t)kRedThreads * U) {
+        f4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * kRedThreads;
+            v[u] = i < n4 ? x4[i] : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            m = absmax_acc(m, v[u].x); m = absmax_acc(m, v[u].y);
+            m = absmax_acc(m, v[u].z); m = absmax_acc(m, v[u].w);
+        }
+    }
+    m = block_max<kRedThreads>(m, red);
+    float s = __fdiv_rn(m, 448.0f);
+    if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
+    uint32_t *y4 = reinterpret_cast<uint32_t *>(y);
+    for (int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kRedThreads)
+        y4[i] = enc4(x4[i], s);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s;
+}
+
+// Scalar fallback (unaligned pointers or n % 4 != 0): amax pass, then an
+// encode pass that re-reads x.
 __global__ __launch_bounds__(kSmallThreads) void k_quantize_dynamic_small(
     const float *__restrict__ x, uint8_t *__restrict__ y, int64_t n, float *__restrict__ scale_out) {
     __shared__ float red[kSmallThreads / 64];
@@ -234,7 +282,9 @@ hipError_t launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s) {
 }
 
 hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream_t s) {
-    hipLaunchKernelGGL(k_amax, dim3(grid_for(n / 4 + 1, 2048)), dim3(kThreads), 0, s, x, n, amax_bits);
+    int64_t g = (n / 4 + (int64_t)kAmaxThreads * kAmaxU - 1) / ((int64_t)kAmaxThreads * kAmaxU);
+    g = g < 1 ? 1 : (g > 256 ? 256 : g);
+    hipLaunchKernelGGL(k_amax, dim3((unsigned)g), dim3(kAmaxThreads), 0, s, x, n, amax_bits);
     return hipGetLastError();
 }
 
@@ -250,8 +300,15 @@ hipError_t launch_amax_to_float(const uint32_t *amax_bits, float *out, hipStream
 hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
                                    uint32_t *work, hipStream_t s) {
     if (n <= kSmallMax) {
-        hipLaunchKernelGGL(k_quantize_dynamic_small, dim3(1), dim3(kSmallThreads), 0, s, x, y, n,
-                           scale_out);
+        if (n % 4 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(y) & 3) == 0) {
+            // one float4 per thread in the encode pass, at most 64 workgroups
+            const int64_t n4 = n / 4;
+            int p = (int)((n4 + kRedThreads - 1) / kRedThreads);
+            p = p < 1 ? 1 : (p > 64 ? 64 : p);
+            hipLaunchKernelGGL(k_quantize_dynamic_spread, dim3(p), dim3(kRedThreads), 0, s, x, y, n4, scale_out);
+        } else
+            hipLaunchKernelGGL(k_quantize_dynamic_small, dim3(1), dim3(kSmallThreads), 0, s, x, y, n,
+                               scale_out);
         return hipGetLastError();
     }
     hipError_t err = launch_fill_u32(work, 0u, 1, s);

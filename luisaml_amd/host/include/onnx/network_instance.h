@@ -1,0 +1,95 @@
+// network_instance.h -- binds a Model to device memory and runs it.
+//
+// Follows the reference's NetworkInstance (include/onnx/network_instance.h:
+// 38-299, src/onnx/network_instance.cpp): external inputs/outputs are bound
+// by name with dtype/shape validation (validate_and_bind, :40-69), weights
+// live in one device weight blob addressed by the initializers' data_offsets
+// (create_tensor_for_var, :202-342, with the FP8 size rule
+// ((n+3)/4)*4 at :222-224), operators come from the OperatorSet and run in
+// node order after set_environment (:641-650).
+//
+// MI355X differences: forward() launches HIP kernels eagerly on one stream
+// (no tracing); prepare() runs once and (1) fuses DequantizeLinear(W_fp8) ->
+// Gemm/MatMul [-> Relu/Gelu], with QuantizeLinear/DynamicQuantizeLinear ->
+// DequantizeLinear on the activation, into one FP8Linear node, and (2) packs
+// every fused FP8 weight into MFMA panels once, at load time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "onnx/onnx.h"
+#include "onnx/tensor_table.h"
+
+namespace lcml::onnx {
+
+// E4M3 weight packed for the GEMM kernels (lcml_fp8_pack_weight) with its
+// fp32 dequantisation scale (1 entry, or N for per-output-channel).
+class PackedWeightTensor : public ITensor {
+    DeviceArray<uint8_t> packed_;
+    DeviceArray<float> scale_;
+    uint32_t K_, N_;
+
+public:
+    PackedWeightTensor(uint32_t K, uint32_t N, DeviceArray<uint8_t> packed, DeviceArray<float> scale)
+        : ITensor(shape_type{K, N}), packed_(std::move(packed)), scale_(std::move(scale)), K_(K), N_(N) {}
+    size_type size() const noexcept override { return K_ * N_; }
+    refl::TypeIndex element_type_index() const noexcept override { return refl::type_index_of<FP8E4M3FN>(); }
+    std::string_view element_type_name() const noexcept override { return "FP8E4M3FN(packed)"; }
+    bool is_constant() const noexcept override { return true; }
+    void *device_data() const noexcept override { return packed_.data(); }
+    uint32_t K() const { return K_; }
+    uint32_t N() const { return N_; }
+    const uint8_t *packed() const { return packed_.data(); }
+    const float *scale() const { return scale_.data(); }
+    bool per_channel() const { return scale_.size() > 1; }
+};
+
+class NetworkInstance {
+    Model model_;
+    TensorTable table_;
+    std::vector<std::unique_ptr<Operator>> ops_;
+    std::vector<size_t> node_order_;
+    hipStream_t stream_ = nullptr;
+    const uint8_t *weight_buffer_ = nullptr;  // device
+    size_t weight_bytes_ = 0;
+    bool fusion_ = true;
+    bool prepared_ = false;
+    size_t fused_count_ = 0;
+    std::vector<std::pair<std::string, std::reference_wrapper<ITensor>>> inputs_, outputs_;
+
+    void create_tensor_for_var(const Variable &var);
+    void validate_and_bind(std::string_view role, const Variable &var, ITensor &t);
+    void fuse_qdq_linear();
+    void pack_weights();
+
+public:
+    NetworkInstance() = default;
+    NetworkInstance(const NetworkInstance &) = delete;
+    NetworkInstance &operator=(const NetworkInstance &) = delete;
+
+    void set_model(Model &&m);
+    const Model &model() const { return model_; }
+    void set_stream(hipStream_t s) { stream_ = s; }
+    hipStream_t stream() const { return stream_; }
+    // Device memory holding the initializers that carry data_offsets.
+    void set_weight_buffer(const void *device_blob, size_t bytes);
+    void set_input(std::string_view name, ITensor &t);
+    void set_output(std::string_view name, ITensor &t);
+    // QDQ -> FP8Linear fusion (default on); off runs every node as written.
+    void set_fusion(bool on) { fusion_ = on; }
+    // The reference's warp-width knob (network_instance.h:50-54); a gfx950
+    // wavefront is 64 lanes and the kernels choose their own launch shapes.
+    uint32_t warp_size() const { return 64; }
+
+    void prepare();
+    void forward();
+    size_t fused_linear_count() const { return fused_count_; }
+    std::vector<std::string> executed_op_types() const;
+    TensorTable &tensor_table() { return table_; }
+};
+
+}  // namespace lcml::onnx

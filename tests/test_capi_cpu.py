@@ -1,0 +1,83 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects invalid arguments with the documented status
+codes before touching the device."""
+import ctypes
+import subprocess
+
+import pytest
+
+from luisaml_amd import capi
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    declared = capi.header_symbols()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert set(declared) <= exported
+    # nothing but the C ABI is exported
+    assert all(s.startswith("lcml_fp8_") for s in exported if not s.startswith("_")), \
+        sorted(s for s in exported if not s.startswith("lcml_fp8_"))[:10]
+
+
+def test_abi_version():
+    assert capi.lib().lcml_fp8_abi_version() == 1
+
+
+def test_packed_weight_bytes():
+    f = capi.lib().lcml_fp8_packed_weight_bytes
+    assert f(128, 64) == 128 * 64
+    assert f(784, 256) == 896 * 256
+    assert f(256, 10) == 256 * 64
+    assert f(4096, 11008) == 4096 * 11008
+    assert f(0, 5) == 0 and f(5, -1) == 0
+
+
+def _gemm(**kw):
+    args = dict(M=4, N=64, K=128, a=0x1000, lda=128, a_scale=0x1000, b=0x1000, b_scale=0x1000, pc=0,
+                alpha=1.0, c=None, c_ndim=0, c0=0, c1=0, beta=1.0, act=0, y=0x1000, y_dtype=1, ldy=64,
+                kernel=0)
+    args.update(kw)
+    return capi.lib().lcml_fp8_gemm(args["M"], args["N"], args["K"], args["a"], args["lda"], args["a_scale"],
+                                    args["b"], args["b_scale"], args["pc"], args["alpha"], args["c"],
+                                    args["c_ndim"], args["c0"], args["c1"], args["beta"], args["act"],
+                                    args["y"], args["y_dtype"], args["ldy"], args["kernel"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(N=0), capi.ERR_INVALID_ARG),
+    (dict(K=-1), capi.ERR_INVALID_ARG),
+    (dict(y_dtype=10), capi.ERR_UNSUPPORTED),
+    (dict(act=9), capi.ERR_UNSUPPORTED),
+    (dict(ldy=10), capi.ERR_INVALID_ARG),
+    (dict(b_scale=None), capi.ERR_INVALID_ARG),
+    (dict(K=100, lda=112), capi.ERR_UNSUPPORTED),
+    (dict(lda=100), capi.ERR_INVALID_ARG),
+    (dict(a=0x1001), capi.ERR_INVALID_ARG),
+    (dict(kernel=99), capi.ERR_INVALID_ARG),
+    (dict(M=17, kernel=capi.KERNEL_SKINNY), capi.ERR_UNSUPPORTED),
+    (dict(c=0x1000, c_ndim=1, c0=7), capi.ERR_INVALID_ARG),
+    (dict(c=0x1000, c_ndim=2, c0=3, c1=64), capi.ERR_INVALID_ARG),
+])
+def test_gemm_argument_validation(kw, code):
+    rc = _gemm(**kw)
+    assert rc == code, capi.last_error()
+    assert capi.last_error()
+
+
+def test_other_entry_point_validation():
+    L = capi.lib()
+    assert L.lcml_fp8_quantize(0x1000, 0x1000, 1, 0, 4, 0x1000, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_quantize(None, None, 1, 1, 0, None, None) == capi.OK  # empty tensor: no-op
+    assert L.lcml_fp8_dequantize(0x1000, None, 1, 1, 4, 0x1000, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_quantize_dynamic(0x1000, 0x1000, 70000, 0x1000, None, None) == capi.ERR_INVALID_ARG
+    assert "workspace" in capi.last_error()
+    assert L.lcml_fp8_pack_weight(0x1000, 0, 64, 0, 0x1000, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_pack_weight(0x1000, 64, 64, 0, 0x1001, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_gemm_w8a32(4, 64, 128, 0x1000, 100, 0x1000, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                                 0x1000, 1, 64, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_gemm(0, 64, 128, None, 128, None, None, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                           0x1000, 1, 64, 0, None) == capi.OK  # M == 0: nothing to do
