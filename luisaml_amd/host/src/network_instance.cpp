@@ -1,0 +1,336 @@
+// network_instance.cpp -- binding, initializer tensors, QDQ fusion, weight
+// packing and eager execution (see network_instance.h).
+#include "onnx/network_instance.h"
+
+#include <algorithm>
+#include <cstring>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "lcml_fp8.h"
+
+namespace lcml::onnx {
+
+namespace {
+
+ITensor::shape_type to_tensor_shape(const std::vector<size_t> &s) {
+    ITensor::shape_type out;
+    for (auto d : s) out.push_back((ITensor::size_type)d);
+    return out;
+}
+
+void hip_check(hipError_t e, const char *what) {
+    LCML_ASSERT(e == hipSuccess, "%s: %s", what, hipGetErrorString(e));
+}
+
+void lcml_check(int rc, const char *what) {
+    LCML_ASSERT(rc == 0, "%s: %s", what, lcml_fp8_last_error());
+}
+
+}  // namespace
+
+void NetworkInstance::set_model(Model &&m) {
+    model_ = std::move(m);
+    prepared_ = false;
+    ops_.clear();
+    table_.clear();
+}
+
+void NetworkInstance::set_weight_buffer(const void *device_blob, size_t bytes) {
+    weight_buffer_ = static_cast<const uint8_t *>(device_blob);
+    weight_bytes_ = bytes;
+}
+
+void NetworkInstance::set_input(std::string_view name, ITensor &t) {
+    inputs_.emplace_back(std::string(name), std::ref(t));
+}
+
+void NetworkInstance::set_output(std::string_view name, ITensor &t) {
+    outputs_.emplace_back(std::string(name), std::ref(t));
+}
+
+// Dtype and shape of an external tensor must match the graph variable
+// (src/onnx/network_instance.cpp:40-69 of the reference).
+void NetworkInstance::validate_and_bind(std::string_view role, const Variable &var, ITensor &t) {
+    LCML_ASSERT(t.element_type_index() == data_type_to_type_index(var.get_dtype()),
+                "%.*s '%s': element type %.*s does not match graph dtype %s", (int)role.size(), role.data(),
+                var.get_name().c_str(), (int)t.element_type_name().size(), t.element_type_name().data(),
+                data_type_name(var.get_dtype()).data());
+    auto shape = to_tensor_shape(var.get_shape());
+    if (!shape.empty()) {
+        LCML_ASSERT(t.shape() == shape, "%.*s '%s': shape mismatch", (int)role.size(), role.data(),
+                    var.get_name().c_str());
+    }
+    table_.bind(var.get_name(), t);
+}
+
+// Initializers (from raw_data or the weight blob) and intermediates
+// (allocated from the variable's static shape), as create_tensor_for_var
+// (src/onnx/network_instance.cpp:202-342).
+void NetworkInstance::create_tensor_for_var(const Variable &var) {
+    if (table_.contains(var.get_name())) return;
+    const auto &name = var.get_name();
+    const size_t n = var.num_elements();
+    auto shape = to_tensor_shape(var.get_shape());
+    visit_type_index<NNTypeList>(data_type_to_type_index(var.get_dtype()), [&]<typename T>() {
+        if (var.is_trainable_weight()) {
+            LCML_ASSERT(weight_buffer_ != nullptr, "Weight buffer not set but required for variable: %s",
+                        name.c_str());
+            auto [start, end] = var.get_buffer_range();
+            LCML_ASSERT(end <= weight_bytes_, "variable %s: data_offsets beyond the weight buffer", name.c_str());
+            if constexpr (std::is_same_v<T, FP8E4M3FN>) {
+                // FP8 blobs are 4-byte padded (network_instance.cpp:222-224)
+                LCML_ASSERT(end - start == ((n + 3) / 4) * 4, "Weight buffer size mismatch for variable: %s",
+                            name.c_str());
+            } else {
+                LCML_ASSERT(end - start == n * sizeof(T), "Weight buffer size mismatch for variable: %s",
+                            name.c_str());
+            }
+            std::vector<uint8_t> host;
+            if (end - start <= 4096) {  // small constants (scales, zero points) get a host copy
+                host.resize(end - start);
+                hip_check(hipMemcpy(host.data(), weight_buffer_ + start, end - start, hipMemcpyDeviceToHost),
+                          "hipMemcpy");
+            }
+            table_.own(name, std::make_unique<ConstTensor<T>>(
+                                 shape, DeviceArray<T>(const_cast<uint8_t *>(weight_buffer_), start, n),
+                                 std::move(host)));
+        } else if (!var.get_raw_data().empty()) {
+            const auto &raw = var.get_raw_data();
+            LCML_ASSERT(raw.size() == n * sizeof(T), "variable %s: raw_data holds %zu bytes, expected %zu",
+                        name.c_str(), raw.size(), n * sizeof(T));
+            DeviceArray<T> arr(n);
+            hip_check(hipMemcpy(arr.data(), raw.data(), raw.size(), hipMemcpyHostToDevice), "hipMemcpy");
+            table_.own(name, std::make_unique<ConstTensor<T>>(shape, std::move(arr),
+                                                              std::vector<uint8_t>(raw.begin(), raw.end())));
+        } else {
+            LCML_ASSERT(!shape.empty() || n == 1, "variable %s has no static shape", name.c_str());
+            table_.own(name, make_device_tensor<T>(shape));
+        }
+    });
+}
+
+// ------------------------------------------------------------------------
+// QDQ fusion:  [x -> QuantizeLinear(s) -> DequantizeLinear(s)] or
+// [x -> DynamicQuantizeLinear -> DequantizeLinear] or plain fp32 A, and
+// DequantizeLinear(W_e4m3 constant, s_w) as B, into Gemm/MatMul, optionally
+// followed by Relu/Gelu, become one FP8Linear node.
+// ------------------------------------------------------------------------
+namespace {
+
+bool is_zero_constant(TensorTable &, const Variable &v) {
+    if (!v.is_constant()) return false;
+    const std::string &raw = v.get_raw_data();
+    if (!raw.empty()) return std::all_of(raw.begin(), raw.end(), [](char c) { return c == 0; });
+    return false;  // zero points in the weight blob are checked when the tensor exists
+}
+
+}  // namespace
+
+void NetworkInstance::fuse_qdq_linear() {
+    Graph &g = model_.mutable_graph();
+    auto &nodes = g.mutable_nodes();
+    std::unordered_map<std::string, size_t> producer;
+    std::unordered_map<std::string, std::vector<size_t>> consumers;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        for (auto &o : nodes[i].get_outputs()) producer[o.get().get_name()] = i;
+        for (auto &in : nodes[i].get_inputs()) consumers[in.get().get_name()].push_back(i);
+    }
+    std::unordered_set<std::string> graph_outputs;
+    for (auto &o : g.get_outputs()) graph_outputs.insert(o.get().get_name());
+    auto only_consumer = [&](const std::string &v, size_t who) {
+        auto it = consumers.find(v);
+        return it != consumers.end() && it->second.size() == 1 && it->second[0] == who && !graph_outputs.count(v);
+    };
+    auto prod = [&](const std::string &v) -> const Node * {
+        auto it = producer.find(v);
+        return it == producer.end() ? nullptr : &nodes[it->second];
+    };
+    auto prod_idx = [&](const std::string &v) { return producer.at(v); };
+
+    std::vector<bool> removed(nodes.size(), false);
+    std::unordered_map<size_t, Node> replacement;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        const Node &n = nodes[i];
+        const bool gemm = n.get_op_type() == "Gemm", matmul = n.get_op_type() == "MatMul";
+        if (!gemm && !matmul) continue;
+        if (gemm && attr_int(n, "transA", 0) != 0) continue;
+        const Variable &A = n.get_inputs()[0].get();
+        const Variable &B = n.get_inputs()[1].get();
+        // ---- B = DequantizeLinear(W_e4m3 constant, s_w [, 0]) ----
+        const Node *dqw = prod(B.get_name());
+        if (!dqw || dqw->get_op_type() != "DequantizeLinear" || !only_consumer(B.get_name(), i)) continue;
+        const Variable &W = dqw->get_inputs()[0].get();
+        const Variable &sw = dqw->get_inputs()[1].get();
+        if (W.get_dtype() != DataType::FLOAT8E4M3FN || !W.is_constant() || W.get_shape().size() != 2) continue;
+        if (!sw.is_constant()) continue;
+        if (dqw->get_inputs().size() > 2 && !is_zero_constant(table_, dqw->get_inputs()[2].get())) continue;
+        const bool w_is_nk = gemm && attr_int(n, "transB", 0) != 0;
+        const size_t N = w_is_nk ? W.get_shape()[0] : W.get_shape()[1];
+        const size_t K = w_is_nk ? W.get_shape()[1] : W.get_shape()[0];
+        const size_t nscale = sw.num_elements();
+        if (nscale != 1) {
+            int axis = attr_int(*dqw, "axis", 1);
+            if (axis < 0) axis += 2;
+            const int n_axis = w_is_nk ? 0 : 1;
+            if (axis != n_axis || nscale != N) continue;  // only per-output-channel scales fuse
+        }
+        if (A.get_shape().empty() || A.get_shape().back() != K) continue;
+        // ---- A: static QDQ, dynamic QDQ, or fp32 ----
+        int a_mode = 0;  // 0: fp32 (W8A32), 1: static scale, 2: dynamic per-tensor
+        const Variable *a_src = &A, *a_scale = nullptr;
+        std::vector<size_t> drop = {prod_idx(B.get_name())};
+        const Node *dqa = prod(A.get_name());
+        if (dqa && dqa->get_op_type() == "DequantizeLinear" && only_consumer(A.get_name(), i)) {
+            const Variable &qv = dqa->get_inputs()[0].get();
+            const Node *q = prod(qv.get_name());
+            // the DQ zero point is a constant 0, or DynamicQuantizeLinear's own (zero) output
+            bool zp_ok = dqa->get_inputs().size() <= 2 || is_zero_constant(table_, dqa->get_inputs()[2].get()) ||
+                         (q && q->get_op_type() == "DynamicQuantizeLinear" && q->get_outputs().size() > 2 &&
+                          &q->get_outputs()[2].get() == &dqa->get_inputs()[2].get());
+            if (q && zp_ok && only_consumer(qv.get_name(), prod_idx(A.get_name())) &&
+                dqa->get_inputs()[1].get().num_elements() == 1) {
+                if (q->get_op_type() == "QuantizeLinear" &&
+                    &q->get_inputs()[1].get() == &dqa->get_inputs()[1].get() &&
+                    (q->get_inputs().size() <= 2 || is_zero_constant(table_, q->get_inputs()[2].get())) &&
+                    attr_int(*q, "saturate", 1) == 1) {
+                    a_mode = 1;
+                    a_src = &q->get_inputs()[0].get();
+                    a_scale = &q->get_inputs()[1].get();
+                } else if (q->get_op_type() == "DynamicQuantizeLinear" &&
+                           &q->get_outputs()[1].get() == &dqa->get_inputs()[1].get()) {
+                    bool private_outputs = true;
+                    for (size_t o = 0; o < q->get_outputs().size(); ++o) {
+                        const auto &on = q->get_outputs()[o].get().get_name();
+                        if (graph_outputs.count(on)) private_outputs = false;
+                        auto it = consumers.find(on);
+                        if (it != consumers.end())
+                            for (size_t c : it->second)
+                                if (c != prod_idx(A.get_name())) private_outputs = false;
+                    }
+                    if (private_outputs) {
+                        a_mode = 2;
+                        a_src = &q->get_inputs()[0].get();
+                    }
+                }
+                if (a_mode) {
+                    drop.push_back(prod_idx(A.get_name()));
+                    drop.push_back(prod_idx(qv.get_name()));
+                }
+            }
+        }
+        if (a_mode == 0 && A.get_dtype() != DataType::FLOAT) continue;
+        // ---- epilogue activation ----
+        const Variable *out = &n.get_outputs()[0].get();
+        int act = LCML_ACT_NONE;
+        auto cit = consumers.find(out->get_name());
+        if (cit != consumers.end() && cit->second.size() == 1 && !graph_outputs.count(out->get_name())) {
+            const Node &r = nodes[cit->second[0]];
+            if (r.get_op_type() == "Relu") act = LCML_ACT_RELU;
+            else if (r.get_op_type() == "Gelu")
+                act = attr_string(r, "approximate", "none") == "tanh" ? LCML_ACT_GELU_TANH : LCML_ACT_GELU_ERF;
+            if (act != LCML_ACT_NONE) {
+                drop.push_back(cit->second[0]);
+                out = &r.get_outputs()[0].get();
+            }
+        }
+        // ---- build the fused node ----
+        std::string pname = W.get_name() + "::packed";
+        if (!g.has_var(pname)) {
+            Variable pv(pname, DataType::FLOAT8E4M3FN, {K, N});
+            pv.set_is_constant(true);
+            g.add_variable(std::move(pv));
+        }
+        Node f(n.get_name().empty() ? "fp8_linear" : n.get_name() + "::fp8", "FP8Linear");
+        f.add_input(*a_src);
+        f.add_input(g.get_var(pname));
+        f.add_input(sw);
+        if (a_mode == 1) f.add_input(*a_scale);
+        const bool has_c = gemm && n.get_inputs().size() > 2;
+        if (has_c) f.add_input(n.get_inputs()[2].get());
+        f.add_output(*out);
+        f.set_attribute(Attribute{"a_mode", (int32_t)a_mode});
+        f.set_attribute(Attribute{"has_c", (int32_t)has_c});
+        f.set_attribute(Attribute{"act", (int32_t)act});
+        f.set_attribute(Attribute{"alpha", gemm ? attr_float(n, "alpha", 1.0f) : 1.0f});
+        f.set_attribute(Attribute{"beta", gemm ? attr_float(n, "beta", 1.0f) : 1.0f});
+        f.set_attribute(Attribute{"w_is_nk", (int32_t)w_is_nk});
+        f.set_attribute(Attribute{"weight", W.get_name()});
+        for (size_t d : drop) removed[d] = true;
+        replacement.emplace(i, std::move(f));
+        ++fused_count_;
+    }
+    if (replacement.empty()) return;
+    std::vector<Node> out;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        auto it = replacement.find(i);
+        if (it != replacement.end()) out.push_back(std::move(it->second));
+        else if (!removed[i]) out.push_back(std::move(nodes[i]));
+    }
+    nodes = std::move(out);
+}
+
+// Load-time packing of every fused weight (north star: weights pre-laid-out
+// at model load into MFMA-fragment order with their fp32 scales).
+void NetworkInstance::pack_weights() {
+    for (const Node &n : model_.get_graph().get_nodes()) {
+        if (n.get_op_type() != "FP8Linear") continue;
+        const Variable &pv = n.get_inputs()[1].get();
+        if (table_.contains(pv.get_name())) continue;
+        const Variable &W = model_.get_graph().get_var(attr_string(n, "weight", ""));
+        const Variable &sw = n.get_inputs()[2].get();
+        create_tensor_for_var(W);
+        create_tensor_for_var(sw);
+        const uint32_t K = (uint32_t)pv.get_shape()[0], N = (uint32_t)pv.get_shape()[1];
+        DeviceArray<uint8_t> packed((size_t)lcml_fp8_packed_weight_bytes(K, N));
+        ITensor &wt = table_.at(W.get_name());
+        lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,
+                                        attr_int(n, "w_is_nk", 0), packed.data(), stream_),
+                   "pack weight");
+        ITensor &st = table_.at(sw.get_name());
+        DeviceArray<float> scale(static_cast<float *>(st.device_data()), 0, st.size());
+        table_.own(pv.get_name(), std::make_unique<PackedWeightTensor>(K, N, std::move(packed), std::move(scale)));
+    }
+}
+
+void NetworkInstance::prepare() {
+    Graph &g = model_.mutable_graph();
+    g.mark_constants();
+    fused_count_ = 0;
+    if (fusion_) fuse_qdq_linear();
+    table_.clear();
+    for (auto &[name, t] : inputs_) validate_and_bind("input", g.get_var(name), t.get());
+    for (auto &[name, t] : outputs_) validate_and_bind("output", g.get_var(name), t.get());
+    pack_weights();
+    for (const Node &n : g.get_nodes()) {
+        for (auto &v : n.get_inputs()) create_tensor_for_var(v.get());
+        for (auto &v : n.get_outputs()) create_tensor_for_var(v.get());
+    }
+    ops_.clear();
+    for (const Node &n : g.get_nodes()) ops_.push_back(model_.get_opset().create_operator(n.get_op_type(), n));
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");  // packing done before first use
+    prepared_ = true;
+}
+
+void NetworkInstance::forward() {
+    if (!prepared_) prepare();
+    const Graph &g = model_.get_graph();
+    for (auto &[name, t] : inputs_) table_.bind(name, t.get());
+    for (auto &[name, t] : outputs_) table_.bind(name, t.get());
+    const auto &nodes = g.get_nodes();
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        std::vector<std::reference_wrapper<ITensor>> ins, outs;
+        for (auto &v : nodes[i].get_inputs()) ins.emplace_back(table_.at(v.get().get_name()));
+        for (auto &v : nodes[i].get_outputs()) outs.emplace_back(table_.at(v.get().get_name()));
+        ops_[i]->set_environment(*this, table_);
+        ops_[i]->forward(ins, outs);
+    }
+}
+
+std::vector<std::string> NetworkInstance::executed_op_types() const {
+    std::vector<std::string> v;
+    for (auto &n : model_.get_graph().get_nodes()) v.push_back(n.get_op_type());
+    return v;
+}
+
+}  // namespace lcml::onnx

@@ -1,0 +1,162 @@
+// Gemm, MatMul, Relu, Gelu and the fused FP8Linear.
+//
+// Gemm: Y = alpha * op(A) op(B) + beta * C with the reference's attributes
+// and defaults (src/onnx/operators/gemm.cpp:365-385) and C broadcast rules
+// (:81-103).  MatMul: 2-D B, A of any rank >= 1 (leading dims flattened into
+// M), as the reference's 2-D path (src/onnx/operators/mat_mul.cpp:45-186).
+// In an fp32 graph both run the plain fp32 kernel (same per-output fma
+// order as the reference); in a QDQ graph the network's fusion pass has
+// already replaced them, with their DequantizeLinear / QuantizeLinear
+// neighbours and a following Relu/Gelu, by FP8Linear.
+#include <vector>
+
+#include "common.h"
+
+namespace lcml::onnx {
+namespace {
+
+using namespace ops;
+
+class Gemm : public StreamOperator {
+    float alpha_, beta_;
+    int transA_, transB_;
+
+public:
+    Gemm(float alpha, float beta, int transA, int transB)
+        : StreamOperator("Gemm"), alpha_(alpha), beta_(beta), transA_(transA), transB_(transB) {}
+    void forward(std::span<std::reference_wrapper<ITensor>> inputs,
+                 std::span<std::reference_wrapper<ITensor>> outputs) override {
+        LCML_ASSERT(inputs.size() >= 2 && inputs.size() <= 3 && outputs.size() == 1,
+                    "Gemm requires 2 or 3 inputs and 1 output.");
+        ITensor &A = inputs[0], &B = inputs[1], &Y = outputs[0];
+        ITensor *C = inputs.size() == 3 ? &inputs[2].get() : nullptr;
+        LCML_ASSERT(A.ndim() == 2 && B.ndim() == 2, "Gemm: A and B must be 2D tensors.");
+        LCML_ASSERT(is_type<float>(A) && is_type<float>(B),
+                    "Gemm: unfused operands must be float (FP8 weights reach Gemm through DequantizeLinear)");
+        const int64_t M = transA_ ? A.shape(1) : A.shape(0), K = transA_ ? A.shape(0) : A.shape(1);
+        const int64_t K2 = transB_ ? B.shape(1) : B.shape(0), N = transB_ ? B.shape(0) : B.shape(1);
+        LCML_ASSERT(K == K2, "Gemm: inner dimensions mismatch (K=%lld vs %lld)", (long long)K, (long long)K2);
+        LCML_ASSERT(Y.ndim() == 2 && Y.shape(0) == M && Y.shape(1) == N, "Gemm: Y shape mismatch");
+        CArgs c = c_args(C);
+        check(lcml_fp8_sgemm(M, N, K, static_cast<const float *>(A.device_data()), A.shape(1), transA_,
+                             static_cast<const float *>(B.device_data()), B.shape(1), transB_, alpha_, c.ptr, c.ndim,
+                             c.d0, c.d1, beta_, LCML_ACT_NONE, Y.device_data(), out_dtype_code(Y, "Gemm"), N, stream_),
+              "Gemm");
+    }
+};
+
+class MatMul : public StreamOperator {
+public:
+    MatMul() : StreamOperator("MatMul") {}
+    void forward(std::span<std::reference_wrapper<ITensor>> inputs,
+                 std::span<std::reference_wrapper<ITensor>> outputs) override {
+        LCML_ASSERT(inputs.size() == 2 && outputs.size() == 1, "MatMul requires 2 inputs and 1 output.");
+        ITensor &A = inputs[0], &B = inputs[1], &Y = outputs[0];
+        LCML_ASSERT(is_type<float>(A) && is_type<float>(B), "MatMul: unfused operands must be float");
+        LCML_ASSERT(B.ndim() == 2, "MatMul: batched B is outside the FP8 linear path");
+        const int64_t K = A.shape(A.ndim() - 1), N = B.shape(1), M = A.size() / K;
+        LCML_ASSERT(B.shape(0) == K, "MatMul: inner dimensions mismatch");
+        check(lcml_fp8_sgemm(M, N, K, static_cast<const float *>(A.device_data()), K, 0,
+                             static_cast<const float *>(B.device_data()), N, 0, 1.0f, nullptr, 0, 0, 0, 0.0f,
+                             LCML_ACT_NONE, Y.device_data(), out_dtype_code(Y, "MatMul"), N, stream_),
+              "MatMul");
+    }
+};
+
+class Activation : public StreamOperator {
+    int act_;
+
+public:
+    Activation(const char *name, int act) : StreamOperator(name), act_(act) {}
+    bool can_operate_inplace() const override { return true; }
+    void forward(std::span<std::reference_wrapper<ITensor>> inputs,
+                 std::span<std::reference_wrapper<ITensor>> outputs) override {
+        ITensor &x = inputs[0], &y = outputs[0];
+        LCML_ASSERT(is_type<float>(x) && is_type<float>(y), "%s: only float tensors are on the FP8 path",
+                    get_name().c_str());
+        LCML_ASSERT(x.size() == y.size(), "%s: input and output must have the same size.", get_name().c_str());
+        check(lcml_fp8_activation(static_cast<const float *>(x.device_data()), static_cast<float *>(y.device_data()),
+                                  x.size(), act_, stream_),
+              get_name().c_str());
+    }
+};
+
+// The fused QDQ linear built by NetworkInstance's fusion pass.
+// inputs: [A, W packed, w_scale, (a_scale if a_mode == 1), (C if has_c)]
+// a_mode 0: A fp32, W8A32 kernel; 1: A quantised with the static a_scale;
+// 2: A quantised with its dynamic per-tensor scale (amax/448).
+class FP8Linear : public StreamOperator {
+    int a_mode_, has_c_, act_;
+    float alpha_, beta_;
+    std::unique_ptr<DeviceBuffer> qa_, sa_, ws_;
+    size_t qa_bytes_ = 0;
+
+public:
+    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta)
+        : StreamOperator("FP8Linear"), a_mode_(a_mode), has_c_(has_c), act_(act), alpha_(alpha), beta_(beta) {}
+    void forward(std::span<std::reference_wrapper<ITensor>> inputs,
+                 std::span<std::reference_wrapper<ITensor>> outputs) override {
+        ITensor &A = inputs[0], &Y = outputs[0];
+        auto *W = dynamic_cast<PackedWeightTensor *>(&inputs[1].get());
+        LCML_ASSERT(W != nullptr, "FP8Linear: input 1 must be a packed weight");
+        LCML_ASSERT(is_type<float>(A), "FP8Linear: A must be float");
+        size_t next = 3;
+        ITensor *a_scale = a_mode_ == 1 ? &inputs[next++].get() : nullptr;
+        ITensor *C = has_c_ ? &inputs[next++].get() : nullptr;
+        const int64_t K = W->K(), N = W->N(), M = A.size() / K;
+        LCML_ASSERT(M * K == (int64_t)A.size(), "FP8Linear: A has %u elements, not a multiple of K=%lld", A.size(),
+                    (long long)K);
+        LCML_ASSERT((int64_t)Y.size() == M * N, "FP8Linear: output size mismatch");
+        CArgs c = c_args(C);
+        const int ydt = out_dtype_code(Y, "FP8Linear");
+        const float *a = static_cast<const float *>(A.device_data());
+        if (a_mode_ == 0) {
+            check(lcml_fp8_gemm_w8a32(M, N, K, a, K, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
+                                      c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, stream_),
+                  "FP8Linear");
+            return;
+        }
+        // quantised activation scratch: M*K E4M3 bytes (16-byte aligned rows need K % 16 == 0)
+        const size_t need = (size_t)(M * K);
+        if (!qa_ || qa_bytes_ < need) {
+            qa_ = std::make_unique<DeviceBuffer>(need);
+            qa_bytes_ = need;
+        }
+        uint8_t *q = static_cast<uint8_t *>(qa_->data());
+        const float *sa;
+        if (a_mode_ == 1) {
+            sa = static_cast<const float *>(a_scale->device_data());
+            check(lcml_fp8_quantize(a, q, 1, 1, M * K, sa, stream_), "FP8Linear quantize");
+        } else {
+            if (!sa_) sa_ = std::make_unique<DeviceBuffer>(sizeof(float));
+            if (!ws_) ws_ = std::make_unique<DeviceBuffer>(LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
+            check(lcml_fp8_quantize_dynamic(a, q, M * K, static_cast<float *>(sa_->data()), ws_->data(), stream_),
+                  "FP8Linear quantize");
+            sa = static_cast<const float *>(sa_->data());
+        }
+        check(lcml_fp8_gemm(M, N, K, q, K, sa, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim, c.d0,
+                            c.d1, beta_, act_, Y.device_data(), ydt, N, LCML_KERNEL_AUTO, stream_),
+              "FP8Linear");
+    }
+};
+
+}  // namespace
+
+REGISTER_TO_DEFAULT_OPSET(Gemm) {
+    return std::make_unique<Gemm>(attr_float(node, "alpha", 1.0f), attr_float(node, "beta", 1.0f),
+                                  attr_int(node, "transA", 0), attr_int(node, "transB", 0));
+};
+REGISTER_TO_DEFAULT_OPSET(MatMul) { return std::make_unique<MatMul>(); };
+REGISTER_TO_DEFAULT_OPSET(Relu) { return std::make_unique<Activation>("Relu", LCML_ACT_RELU); };
+REGISTER_TO_DEFAULT_OPSET(Gelu) {
+    std::string approx = attr_string(node, "approximate", "none");
+    LCML_ASSERT(approx == "none" || approx == "tanh", "Gelu: unsupported approximate attribute: %s", approx.c_str());
+    return std::make_unique<Activation>("Gelu", approx == "tanh" ? LCML_ACT_GELU_TANH : LCML_ACT_GELU_ERF);
+};
+REGISTER_TO_DEFAULT_OPSET(FP8Linear) {
+    return std::make_unique<FP8Linear>(attr_int(node, "a_mode", 0), attr_int(node, "has_c", 0),
+                                       attr_int(node, "act", 0), attr_float(node, "alpha", 1.0f),
+                                       attr_float(node, "beta", 1.0f));
+};
+
+}  // namespace lcml::onnx

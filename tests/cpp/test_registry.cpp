@@ -1,0 +1,128 @@
+// test_registry.cpp -- host-layer checks that need no GPU, in the manner of
+// the reference's tests/onnx/test_onnx_import.cpp: the default operator set,
+// JSON import of the reference's own MLP fixture, operator creation from
+// the imported nodes, the tensor API and the error behaviour.
+//   usage: test_registry <tests/golden dir>
+#include <cstdio>
+#include <fstream>
+#include <sstream>
+#include <string>
+#include <cstring>
+
+#include "onnx/network_instance.h"
+#include "onnx/onnx.h"
+#include "onnx/tensor.h"
+
+using namespace lcml::onnx;
+
+static int failures = 0;
+#define CHECK(c)                                                        \
+    do {                                                                \
+        if (!(c)) {                                                     \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #c);    \
+            ++failures;                                                 \
+        }                                                               \
+    } while (0)
+
+template <typename F>
+static bool throws(F &&f) {
+    try {
+        f();
+    } catch (const Error &) {
+        return true;
+    }
+    return false;
+}
+
+static std::string read_text(const std::string &path) {
+    std::ifstream f(path);
+    std::stringstream ss;
+    ss << f.rdbuf();
+    return ss.str();
+}
+
+int main(int argc, char **argv) {
+    if (argc < 2) {
+        std::printf("usage: test_registry <golden dir>\n");
+        return 2;
+    }
+    const std::string golden = argv[1];
+    auto &opset = OperatorSet::get_default();
+    CHECK(opset.get_domain() == "default" && opset.get_version() == 21);
+    for (const char *op : {"Gemm", "MatMul", "QuantizeLinear", "DequantizeLinear", "DynamicQuantizeLinear", "Cast",
+                           "Relu", "Gelu", "FP8Linear"})
+        CHECK(opset.has_operator(op));
+    CHECK(!opset.has_operator("NotAnOp"));
+    Node bogus("n", "NotAnOp");
+    CHECK(throws([&] { opset.create_operator("NotAnOp", bogus); }));
+
+    // ---- import the reference's fixture graph ----
+    Model m = Model::load_from_json(read_text(golden + "/simple_mlp.onnx.json"));
+    const Graph &g = m.get_graph();
+    CHECK(g.get_nodes().size() == 5);
+    const char *ops[] = {"Gemm", "Relu", "Gemm", "Relu", "Gemm"};
+    for (size_t i = 0; i < g.get_nodes().size() && i < 5; ++i) CHECK(g.get_nodes()[i].get_op_type() == ops[i]);
+    CHECK(g.get_inputs().size() == 1 && g.get_inputs()[0].get().get_name() == "input");
+    CHECK((g.get_inputs()[0].get().get_shape() == std::vector<size_t>{1, 784}));
+    CHECK((g.get_outputs()[0].get().get_shape() == std::vector<size_t>{1, 10}));
+    const Variable &w0 = g.get_var("net.0.weight");
+    CHECK(w0.get_dtype() == DataType::FLOAT && w0.is_trainable_weight() && w0.is_constant());
+    CHECK((w0.get_shape() == std::vector<size_t>{256, 784}));
+    CHECK((w0.get_buffer_range() == std::pair<uint64_t, uint64_t>{1024, 803840}));
+    const Node &gemm0 = g.get_nodes()[0];
+    CHECK(attr_int(gemm0, "transB", 0) == 1 && attr_int(gemm0, "transA", 1) == 0);
+    CHECK(attr_float(gemm0, "alpha", 0.f) == 1.0f && attr_float(gemm0, "beta", 0.f) == 1.0f);
+    CHECK(!g.get_var("linear").is_constant() && !g.get_var("input").is_constant());
+    for (const Node &n : g.get_nodes()) {
+        auto op = opset.create_operator(n.get_op_type(), n);
+        CHECK(op && op->get_name() == n.get_op_type() && !op->is_output_view(0, n));
+    }
+
+    // ---- attribute kinds and malformed graphs ----
+    Model a = Model::load_from_json(R"({"ir_version": 10, "graph": {"name": "g",
+        "input": [{"name": "x", "type": {"tensor_type": {"elem_type": "FLOAT", "shape": {"dim": [{"dim_value": "4"}]}}}}],
+        "output": [{"name": "y", "type": {"tensor_type": {"elem_type": "FLOAT", "shape": {"dim": [{"dim_value": "4"}]}}}}],
+        "node": [{"op_type": "Gelu", "input": ["x"], "output": ["y"],
+                  "attribute": [{"name": "approximate", "s": "dGFuaA==", "type": "STRING"},
+                                {"name": "ks", "ints": ["3", "3"], "type": "INTS"},
+                                {"name": "fs", "floats": [0.5, 2], "type": "FLOATS"}]}]}})");
+    const Node &gel = a.get_graph().get_nodes()[0];
+    CHECK(attr_string(gel, "approximate", "") == "tanh");
+    CHECK((gel.get_attribute("ks").get<AttributeType::INTS>() == std::vector<int32_t>{3, 3}));
+    CHECK((gel.get_attribute("fs").get<AttributeType::FLOATS>() == std::vector<float>{0.5f, 2.0f}));
+    CHECK(throws([&] { gel.get_attribute("missing"); }));
+    CHECK(throws([&] { (void)gel.get_attribute("ks").get<AttributeType::FLOAT>(); }));
+    CHECK(throws([] { Model::load_from_json(R"({"graph": {"node": [{"op_type": "NotAnOp", "input": [], "output": ["y"]}]}})"); }));
+    CHECK(throws([] { Model::load_from_json(R"({"graph": {"node": [)"); }));
+    CHECK(throws([] { Model::load_from_json(R"({"graph": {"initializer": [{"name": "w", "data_type": "BOGUS"}]}})"); }));
+    {
+        Model e = Model::load_from_json(R"({"graph": {"initializer": [{"name": "s", "data_type": "FLOAT", "raw_data": "AACAPw=="}]}})");
+        const Variable &s = e.get_graph().get_var("s");
+        CHECK((s.get_shape() == std::vector<size_t>{1}) && s.get_raw_data().size() == 4);  // shape [1] without dims
+        float v;
+        std::memcpy(&v, s.get_raw_data().data(), 4);
+        CHECK(v == 1.0f);
+    }
+
+    // ---- tensor API (borrowed storage: no device allocation) ----
+    float dummy[24];
+    Tensor<float> t({2, 3, 4}, DeviceArray<float>(dummy, 0, 24));
+    CHECK((t.strides() == ITensor::shape_type{12, 4, 1}) && t.ndim() == 3 && t.size() == 24);
+    CHECK((t.unravel_index(17) == std::vector<uint32_t>{1, 1, 1}) && t.linear_index({1, 2, 3}) == 23);
+    CHECK(t.element_type_name() == "float" && t.element_type_index() == refl::type_index_of<float>());
+    CHECK(refl::type_index_of<float>() != refl::type_index_of<FP8E4M3FN>());
+    CHECK(data_type_to_type_index(DataType::FLOAT8E4M3FN) == refl::type_index_of<FP8E4M3FN>());
+    CHECK(!t.is_constant() && !t.is_view() && t.container().is_byte_buffer() && t.container().get_byte_offset() == 0);
+    t.reshape({6, 4});
+    CHECK((t.strides() == ITensor::shape_type{4, 1}));
+    CHECK(throws([&] { Tensor<float> bad({5}, DeviceArray<float>(dummy, 0, 4)); }));
+    int visited = 0;
+    visit_type_index<NNTypeList>(refl::type_index_of<FP8E4M3FN>(), [&]<typename T>() {
+        visited = std::is_same_v<T, FP8E4M3FN> ? 1 : -1;
+    });
+    CHECK(visited == 1);
+    CHECK(throws([] { visit_type_index<NNTypeList>(12345, []<typename T>() {}); }));
+
+    std::printf(failures ? "FAILED (%d)\n" : "PASS\n", failures);
+    return failures ? 1 : 0;
+}
