@@ -153,6 +153,15 @@ def main() -> int:
     g_gemm.replay()
     gemm_ms_total = timed(g_gemm.replay) / args.steps  # three GEMM launches per step
     bytes_step = sum(small_m_bytes(M) for M in SMALL_MS)
+    # HBM bytes per launch of the GEMM kernel, from the committed counter runs
+    # (FETCH_SIZE / WRITE_SIZE per dispatch, copy-calibrated); None if absent
+    traffic_bytes, traffic_src = None, None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "skinny_gemm_small_m_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            tj = json.load(fh)
+        traffic_bytes = tj["mean_hbm_bytes"]
+        traffic_src = "profiles/skinny_gemm_small_m_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, mean over M)"
     value_gbs = bytes_step / (step_ms * 1e-3) / 1e9
     kbytes = sum(gemm_kernel_bytes(M) for M in SMALL_MS)
     k_gbs = kbytes / (gemm_ms_total * 1e-3) / 1e9
@@ -172,7 +181,8 @@ def main() -> int:
                    "bytes_per_step": bytes_step, "pct_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm", "kernel": "k_gemm_skinny (exact bf16-MFMA instantiation)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
+                     "traffic_source": traffic_src,
                      "bytes_per_launch": {str(M): gemm_kernel_bytes(M) for M in SMALL_MS},
                      "avg_launch_us": {str(M): per_launch[str(M)] for M in SMALL_MS},
                      "avg_launch_us_all": round(1e3 * gemm_ms_total / 3, 2)},

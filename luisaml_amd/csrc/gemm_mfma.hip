@@ -44,18 +44,34 @@
 namespace lcml {
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int NT = 512;
-constexpr int A_BYTES = BM * BK;
-constexpr int B_BYTES = BN * BK;
-constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr int EP_PITCH = 33;  // epilogue staging row pitch (floats)
-constexpr int LDS_BYTES = 2 * STAGE > 8 * 128 * EP_PITCH * 4 ? 2 * STAGE : 8 * 128 * EP_PITCH * 4;
+#ifndef LCML_GEMM_WAVES_M
+#define LCML_GEMM_WAVES_M 2
+#endif
+#ifndef LCML_GEMM_WAVES_N
+#define LCML_GEMM_WAVES_N 4
+#endif
+
+constexpr int BK = 128;
 constexpr int GROUP_M = 8;
+constexpr int EP_PITCH = 33;  // epilogue staging row pitch (floats)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// Tile geometry: WAVES_M x WAVES_N wavefronts, each owning WM x WN blocks of
+// 32x32 outputs; the workgroup tile is 256x256 in both shipped layouts
+// (2x4 wavefronts of 128x64, or 2x2 wavefronts of 128x128).
+template <int WAVES_M, int WAVES_N, int WM, int WN>
+struct Tile {
+    static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
+    static constexpr int BM = WAVES_M * WM * 32, BN = WAVES_N * WN * 32;
+    static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_BLK = BM / 8 / NW, B_BLK = BN / 8 / NW;  // 1 KB load blocks per wavefront
+    static constexpr int EP_BYTES = NW * WM * 32 * EP_PITCH * 4;
+    static constexpr int LDS_BYTES = 2 * STAGE > EP_BYTES ? 2 * STAGE : EP_BYTES;
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && (BM / 8) % NW == 0 && (BN / 8) % NW == 0, "tile shape");
+};
 
 struct GemmArgs {
     int64_t M, N, K;
@@ -82,11 +98,12 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 
 __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <bool EXACT>
-__global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
+template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT>
+__global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs g) {
+    using T = Tile<WAVES_M, WAVES_N, WM, WN>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
     // ---- tile selection -------------------------------------------------
     const int ntiles = g.tiles_m * g.tiles_n;
@@ -98,57 +115,64 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
     const int gsize = min(g.tiles_m - first_m, GROUP_M);
     const int tm = first_m + (t % per_group) % gsize;
     const int tn = (t % per_group) / gsize;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * T::BM, n0 = (int64_t)tn * T::BN;
 
     // ---- global -> LDS block assignment ----------------------------------
-    // Wavefront w moves A blocks 4w..4w+3 (8 rows each) and B blocks
-    // 4w..4w+3 (panel b/8, k-chunk b%8) of every K step.
+    // A: 1 KB block b holds rows 8b..8b+7; B: block b holds panel b/8, k-chunk b%8.
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, (int)g.a_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t b_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.bp, 0, (int)g.b_bytes, 0x00020000);
-    uint32_t a_off[4];
-    int a_kc[4];
-    uint32_t b_off[4];
+    uint32_t a_off[T::A_BLK];
+    int a_kc[T::A_BLK];
+    uint32_t b_off[T::B_BLK];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (wave * 4 + i) * 8 + (lane >> 3);
+    for (int i = 0; i < T::A_BLK; ++i) {
+        const int r = (wave * T::A_BLK + i) * 8 + (lane >> 3);
         const int c = (lane & 7) ^ ((r >> 1) & 7);
         a_kc[i] = c * 16;
         a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
-        const int b = wave * 4 + i;
+    }
+#pragma unroll
+    for (int i = 0; i < T::B_BLK; ++i) {
+        const int b = wave * T::B_BLK + i;
         const int64_t panel = (n0 >> 6) + (b >> 3);
         b_off[i] = panel < g.npanels ? (uint32_t)((panel * g.KC + (b & 7)) * 1024 + lane * 16) : OOB;
     }
     auto issue_tile = [&](int kt, int stage) {
-        uint8_t *sa = smem + stage * STAGE;
+        uint8_t *sa = smem + stage * T::STAGE;
         const uint32_t kbyte = (uint32_t)kt * BK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < T::A_BLK; ++i) {
             const uint32_t off =
                 (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * 4 + i) * 1024), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * T::A_BLK + i) * 1024), 16,
                                                      off, 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < T::B_BLK; ++i) {
             const uint32_t off = b_off[i] != OOB ? b_off[i] + (uint32_t)kt * 8 * 1024 : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                b_rsrc, (lds_void *)(sa + A_BYTES + (wave * 4 + i) * 1024), 16, off, 0, 0, 0);
+                b_rsrc, (lds_void *)(sa + T::A_BYTES + (wave * T::B_BLK + i) * 1024), 16, off, 0, 0, 0);
         }
     };
 
-    v16f acc[4][2];
+    v16f acc[WM][WN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int kgrp = (lane >> 5) * 2;  // first k-chunk of this lane within a 64-k block
-    const int a_r0 = wm * 128 + (lane & 31);
-    const int b_col_off = wn * 8192 + (lane & 31) * 16;
+    const int a_r0 = wm * WM * 32 + (lane & 31);
+    int b_off_lds[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const int col = wn * WN * 32 + j * 32;  // first column of this 32-column block in the tile
+        b_off_lds[j] = (col >> 6) * 8192 + ((col & 63) + (lane & 31)) * 16;
+    }
 
     issue_tile(0, 0);
     __syncthreads();
@@ -156,41 +180,48 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
     for (int kt = 0; kt < g.nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < g.nk) issue_tile(kt + 1, cur ^ 1);
-        const uint8_t *sa = smem + cur * STAGE;
-        const uint8_t *sb = sa + A_BYTES;
+        const uint8_t *sa = smem + cur * T::STAGE;
+        const uint8_t *sb = sa + T::A_BYTES;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int c0 = s * 4 + kgrp;
-            v8i bf[2];
+            v8i bf[WN], af[WM];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint8_t *p = sb + b_col_off + j * 32 * 16 + c0 * 1024;
+            for (int j = 0; j < WN; ++j) {
+                const uint8_t *p = sb + b_off_lds[j] + c0 * 1024;
                 bf[j] = join(*reinterpret_cast<const u4 *>(p), *reinterpret_cast<const u4 *>(p + 1024));
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < WM; ++i) {
                 const int r = a_r0 + i * 32;
-                v8i af = join(*reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0)),
-                              *reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0 + 1)));
-                if constexpr (EXACT) {
-                    // 64 k of this lane's fragment = 4 groups of 8; group q feeds
-                    // the q-th 32x32x16 bf16 MFMA for both operands (the same k
-                    // permutation on A and B, so the dot product is unchanged).
+                af[i] = join(*reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0)),
+                             *reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0 + 1)));
+            }
+            if constexpr (EXACT) {
+                // 64 k of each lane's fragment = 4 groups of 8; group q feeds the
+                // q-th 32x32x16 bf16 MFMA for both operands (the same k
+                // permutation on A and B, so the dot product is unchanged).  The
+                // WM*WN MFMAs of one group are independent of each other.
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const bf16x8 a16 = e4m3x8_to_bf16((uint32_t)af[2 * q], (uint32_t)af[2 * q + 1]);
+                for (int q = 0; q < 4; ++q) {
+                    bf16x8 a16[WM], b16[WN];
 #pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                a16, e4m3x8_to_bf16((uint32_t)bf[j][2 * q], (uint32_t)bf[j][2 * q + 1]),
-                                acc[i][j], 0, 0, 0);
-                    }
-                } else {
+                    for (int i = 0; i < WM; ++i) a16[i] = e4m3x8_to_bf16((uint32_t)af[i][2 * q], (uint32_t)af[i][2 * q + 1]);
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[i][j], 0, 0,
-                                                                                    0, 0, 0, 0);
+                    for (int j = 0; j < WN; ++j) b16[j] = e4m3x8_to_bf16((uint32_t)bf[j][2 * q], (uint32_t)bf[j][2 * q + 1]);
+#pragma unroll
+                    for (int i = 0; i < WM; ++i)
+#pragma unroll
+                        for (int j = 0; j < WN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
                 }
+            } else {
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0,
+                                                                                    0, 0, 0);
             }
         }
         __syncthreads();
@@ -198,27 +229,27 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
 
     // ---- epilogue --------------------------------------------------------
     // The accumulators go through LDS (free after the last barrier) one
-    // 32-column half of the wavefront tile at a time, so the epilogue runs as
-    // one rolled loop with a fixed column per lane instead of 128 unrolled
+    // 32-column block of the wavefront tile at a time, so the epilogue runs
+    // as one rolled loop with a fixed column per lane instead of unrolled
     // copies of the activation code.  Row pitch 33 floats keeps the
     // 2-row-per-instruction writes conflict free.
     const Epilogue &e = g.e;
     const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
-    float *st = reinterpret_cast<float *>(smem) + wave * (128 * EP_PITCH);
+    float *st = reinterpret_cast<float *>(smem) + wave * (WM * 32 * EP_PITCH);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < WN; ++j) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EP_PITCH + (lane & 31)] = acc[i][j][r];
         __syncthreads();
-        const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+        const int64_t col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
         if (col < e.N) {
             const float sc = epi_scale(e, a_s, col);
-            const int64_t row0 = m0 + wm * 128 + (lane >> 5);
+            const int64_t row0 = m0 + wm * WM * 32 + (lane >> 5);
 #pragma unroll 1
-            for (int q = 0; q < 64; ++q) {
+            for (int q = 0; q < WM * 16; ++q) {
                 const int64_t row = row0 + 2 * q;
                 if (row >= e.M) break;
                 epi_store(e, row, col, epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
@@ -228,16 +259,19 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_mfma(GemmArgs g) {
     }
 }
 
+constexpr int WAVES_M = LCML_GEMM_WAVES_M, WAVES_N = LCML_GEMM_WAVES_N;
+constexpr int WM = 256 / 32 / WAVES_M, WN = 256 / 32 / WAVES_N;
+using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
 bool g_attr_set[2] = {false, false};
 
 }  // namespace
 
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                             const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
-    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_mfma<true>)
-                           : reinterpret_cast<const void *>(k_gemm_mfma<false>);
+    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, true>)
+                           : reinterpret_cast<const void *>(k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, false>);
     if (!g_attr_set[exact]) {
-        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Shipped::LDS_BYTES);
         if (err != hipSuccess) return err;
         g_attr_set[exact] = true;
     }
@@ -246,16 +280,18 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
     int64_t Kp = pad_to(K, kPackK), Np = pad_to(N, kPanelCols);
     g.KC = Kp / 16;
     g.npanels = Np / 64;
-    g.tiles_m = (int)((M + BM - 1) / BM);
-    g.tiles_n = (int)((N + BN - 1) / BN);
+    g.tiles_m = (int)((M + Shipped::BM - 1) / Shipped::BM);
+    g.tiles_n = (int)((N + Shipped::BN - 1) / Shipped::BN);
     g.nk = (int)(Kp / BK);
     g.a_bytes = (uint32_t)((M - 1) * lda + K);
     g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
     g.e = e;
     if (exact)
-        hipLaunchKernelGGL(k_gemm_mfma<true>, dim3(g.tiles_m * g.tiles_n), dim3(NT), LDS_BYTES, s, g);
+        hipLaunchKernelGGL((k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, true>), dim3(g.tiles_m * g.tiles_n),
+                           dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
     else
-        hipLaunchKernelGGL(k_gemm_mfma<false>, dim3(g.tiles_m * g.tiles_n), dim3(NT), LDS_BYTES, s, g);
+        hipLaunchKernelGGL((k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, false>), dim3(g.tiles_m * g.tiles_n),
+                           dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
     return hipGetLastError();
 }
 
