@@ -160,6 +160,35 @@ LCML_API int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, in
                   int64_t ldy, int kernel, void *stream);
 
 /*
+ * Linear with dynamic per-tensor activation quantisation, one call:
+ *   s = amax(x) / 448 (1 when that is not a positive finite number),
+ *   Y = act( alpha * (DQ(Q(x, s)) x DQ(W)) + beta * C )
+ * i.e. DynamicQuantizeLinear(x) -> DequantizeLinear -> Gemm/MatMul with the
+ * packed E4M3 weight and its scales, bit-identical to
+ * lcml_fp8_quantize_dynamic followed by lcml_fp8_gemm.
+ * x: fp32 [M, K] row-major, row pitch ldx elements.
+ * With kernel LCML_KERNEL_SKINNY or SKINNY_FP8, M <= 16, x 16-byte aligned,
+ * ldx % 4 == 0 and M * (K rounded up to 128, + 16) <= 96 KiB, one fused
+ * kernel quantises x on the fly and needs no workspace; LCML_KERNEL_AUTO
+ * fuses under the same conditions when also M * K <= 8192 (each workgroup
+ * of the fused kernel encodes all of x).  Otherwise x must be
+ * contiguous (ldx == K) and the call quantises into `workspace`
+ * (lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel) bytes) and runs the
+ * GEMM selected by `kernel`.
+ * x_scale_out: optional device float that receives s.
+ * Epilogue arguments and y as for lcml_fp8_gemm.
+ * The reference has no dynamic quantiser; this replaces the composition
+ * Abs -> ReduceMax (src/onnx/operators/reduce.cpp:417-459) -> Div -> Cast
+ * (src/onnx/operators/cast.cpp:63-67) feeding Gemm (gemm.cpp:27-325).
+ */
+LCML_API int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel);
+LCML_API int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                          const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel,
+                          float alpha, const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1,
+                          float beta, int act, void *y, int y_dtype, int64_t ldy, float *x_scale_out,
+                          void *workspace, int64_t workspace_bytes, int kernel, void *stream);
+
+/*
  * W8A32 linear: fp32 activations times packed E4M3 weights, same epilogue:
  *   y[m,n] = act( alpha * (sum_k a[m,k] * to_float(B[k,n])) * b_scale[n|0]
  *                 + beta * C )

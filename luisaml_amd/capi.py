@@ -46,6 +46,9 @@ _SIGS = {
     "lcml_fp8_unpack_weight": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "lcml_fp8_gemm": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
                              _i64, _i64, _f32, _int, _vp, _int, _i64, _int, _vp]),
+    "lcml_fp8_gemm_dynamic_workspace_bytes": (_i64, [_i64, _i64, _int]),
+    "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
+                                     _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
     "lcml_fp8_gemm_w8a32": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int,
                                    _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
     "lcml_fp8_sgemm": (_int, [_i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _f32, _vp, _int, _i64,
@@ -208,6 +211,31 @@ def gemm(a: torch.Tensor, a_scale: torch.Tensor, b_packed: torch.Tensor, b_scale
                                _ptr(b_scale), per_ch, float(alpha), _ptr(cc), nd, c0, c1,
                                float(beta), int(act), _ptr(y), ydt, y.stride(0), int(kernel),
                                _stream(stream)))
+    return y
+
+
+def gemm_dynamic(x: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor, N: int, K: int,
+                 c: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 1.0, act: int = ACT_NONE,
+                 out_dtype=torch.float32, kernel: int = KERNEL_AUTO, out: torch.Tensor | None = None,
+                 scale_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                 stream=None) -> torch.Tensor:
+    """DynamicQuantizeLinear(x) -> FP8 linear in one call: x [M,K] fp32 -> [M,N].
+    The workspace (uint8, allocated here when needed and not given) is only
+    used when the fused small-M kernel does not apply."""
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+    M = x.shape[0]
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x.device)
+    ydt = _DTYPE_CODE.get(y.dtype, 0)
+    cc, nd, c0, c1 = _c_args(c)
+    per_ch = int(b_scale.numel() > 1)
+    need = lib().lcml_fp8_gemm_dynamic_workspace_bytes(M, K, int(kernel))
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    _check(lib().lcml_fp8_gemm_dynamic(M, N, K, _ptr(x), x.stride(0), _ptr(b_packed), _ptr(b_scale), per_ch,
+                                       float(alpha), _ptr(cc), nd, c0, c1, float(beta), int(act), _ptr(y), ydt,
+                                       y.stride(0), _ptr(scale_out), _ptr(workspace), ws_bytes, int(kernel),
+                                       _stream(stream)))
     return y
 
 

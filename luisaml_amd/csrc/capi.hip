@@ -186,6 +186,65 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     return hip_status(err, fn);
 }
 
+namespace {
+// The fused kernel applies when the quantised activations fit its LDS copy.
+// Every workgroup of it reads and encodes all M*K activations; on the
+// 4096x11008 linear that redundant pass beats the separate quantise launch
+// up to M = 2, so AUTO fuses while M*K <= 8192.
+constexpr int64_t kAutoFuseMaxElems = 8192;
+bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kernel) {
+    const bool fits = M <= 16 && lcml::skinny_dynamic_lds_bytes(M, K) <= lcml::kSkinnyDynLdsMax &&
+                      (!x || aligned(x, 16)) && ldx % 4 == 0;
+    if (kernel == LCML_KERNEL_AUTO) return fits && M * K <= kAutoFuseMaxElems;
+    return fits && (kernel == LCML_KERNEL_SKINNY || kernel == LCML_KERNEL_SKINNY_FP8);
+}
+int64_t pad256(int64_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
+int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel) {
+    if (M <= 0 || K <= 0) return 0;
+    if (dynamic_fusable(M, K, nullptr, K, kernel)) return 0;
+    // quantised activations, the amax word block, the scale (when not returned)
+    return pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256;
+}
+
+int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx, const uint8_t *b_packed,
+                          const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
+                          int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                          float *x_scale_out, void *workspace, int64_t workspace_bytes, int kernel, void *stream) {
+    const char *fn = "lcml_fp8_gemm_dynamic";
+    if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
+                                               (long long)M, (long long)N, (long long)K);
+    lcml::Epilogue e;
+    if (int rc = make_epilogue(e, fn, M, N, nullptr, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                               c_dim1, beta, act, y, y_dtype, ldy))
+        return rc;
+    if (M == 0) return LCML_OK;
+    if (!x || !b_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (K % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", fn, (long long)K);
+    if (ldx < K) return fail(LCML_ERR_INVALID_ARG, "%s: ldx=%lld < K=%lld", fn, (long long)ldx, (long long)K);
+    if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
+    hipStream_t s = (hipStream_t)stream;
+    if (dynamic_fusable(M, K, x, ldx, kernel))
+        return hip_status(lcml::launch_gemm_skinny_dynamic(M, N, K, x, ldx, b_packed, e, x_scale_out,
+                                                           kernel != LCML_KERNEL_SKINNY_FP8, s),
+                          fn);
+    // two-step path: quantise into the workspace, then the selected GEMM
+    if (ldx != K) return fail(LCML_ERR_UNSUPPORTED, "%s: x must be contiguous (ldx == K) for M=%lld", fn, (long long)M);
+    const int64_t need = lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return fail(LCML_ERR_INVALID_ARG, "%s: needs a 256-byte aligned workspace of %lld bytes", fn,
+                    (long long)need);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    uint8_t *q = ws;
+    uint32_t *amax_word = reinterpret_cast<uint32_t *>(ws + pad256(M * K));
+    float *scale = x_scale_out ? x_scale_out : reinterpret_cast<float *>(ws + pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
+    hipError_t err = lcml::launch_quantize_dynamic(x, q, M * K, scale, amax_word, s);
+    if (err != hipSuccess) return hip_status(err, fn);
+    return lcml_fp8_gemm(M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                         c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
+}
+
 int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, const uint8_t *b_packed,
                         const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
                         int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,

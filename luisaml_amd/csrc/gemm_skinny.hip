@@ -17,6 +17,19 @@
 // v_mfma_f32_16x16x32_bf16 (fp32-accurate accumulation).  FAST: one
 // v_mfma_f32_16x16x128_f8f6f4 on the raw bytes (gfx950 FP8 MFMAs truncate
 // products far below the block maximum; opt-in).
+//
+// DYN (fused DynamicQuantizeLinear): the activations arrive as fp32 and are
+// quantised inside the kernel.  Every workgroup first starts the loads of
+// its first two weight K blocks per wavefront, then reduces amax = max|x| over the whole
+// activation matrix (L2-resident: all workgroups read the same M*K floats),
+// derives the per-tensor scale amax/448 exactly as the standalone dynamic
+// quantiser does, and encodes the rows into LDS (row pitch Kp+16 bytes, so
+// the 16 rows of a fragment read fall in distinct banks; k >= K is zero).
+// The main loop then reads the activation operand from LDS.  The redundant
+// per-workgroup amax and encode cost M*K loads and ~20 VALU operations per
+// element in every workgroup (measured on the 4096x11008 linear: +2.7 us at
+// M=1, +6 us at M=4 over the GEMM alone, against +4.5 us for the separate
+// quantise launch), so the fused kernel only pays off for small M*K.
 #include "lcml_internal.hpp"
 
 namespace lcml {
@@ -40,6 +53,9 @@ struct SkinnyArgs {
     int64_t M, N, K;
     const uint8_t *a;
     int64_t lda;
+    const float *x;     // DYN: fp32 activations [M, K], row stride ldx elements
+    int64_t ldx;
+    float *scale_out;   // DYN: optional, receives the dynamic scale
     const uint8_t *bp;
     int64_t KC;      // k-chunks per panel
     int64_t nblk16;  // 16-column blocks in the packed matrix (Np / 16)
@@ -54,10 +70,13 @@ __device__ inline v8i join(u4 lo, u4 hi) {
     return r;
 }
 
-template <int NB, int WAVES, int UNROLL, bool EXACT>
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int NB, int WAVES, int UNROLL, bool EXACT, bool DYN>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     constexpr int NT = WAVES * 64;
     __shared__ v4f red[WAVES][NB][64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // DYN: [M][pitch] E4M3
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t blk0 = (int64_t)blockIdx.x * NB;  // first 16-column block
 
@@ -103,11 +122,25 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
                 f.blo[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(p)) : u4{0, 0, 0, 0};
                 f.bhi[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(p + 1024)) : u4{0, 0, 0, 0};
             }
-            const int64_t k = (int64_t)kb * 128 + (lane >> 4) * 32;
-            const bool ok_lo = in && a_ok && k < g.K;
-            const bool ok_hi = in && a_ok && k + 16 < g.K;
-            f.alo[u] = ok_lo ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128) : u4{0, 0, 0, 0};
-            f.ahi[u] = ok_hi ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128 + 16) : u4{0, 0, 0, 0};
+            if constexpr (!DYN) {
+                const int64_t k = (int64_t)kb * 128 + (lane >> 4) * 32;
+                const bool ok_lo = in && a_ok && k < g.K;
+                const bool ok_hi = in && a_ok && k + 16 < g.K;
+                f.alo[u] = ok_lo ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128) : u4{0, 0, 0, 0};
+                f.ahi[u] = ok_hi ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128 + 16) : u4{0, 0, 0, 0};
+            }
+        }
+    };
+    // DYN: activation fragments from the LDS copy (zero-padded to Kp)
+    const int64_t pitch = pad_to(g.K, kPackK) + 16;
+    auto read_a = [&](Frag &f, int kb0) {
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int kb = kb0 + u;
+            const uint8_t *p = a_lds + (a_ok ? arow : 0) * pitch + (int64_t)kb * 128 + (lane >> 4) * 32;
+            const bool ok = a_ok && kb < kb_end;
+            f.alo[u] = ok ? *reinterpret_cast<const u4 *>(p) : u4{0, 0, 0, 0};
+            f.ahi[u] = ok ? *reinterpret_cast<const u4 *>(p + 16) : u4{0, 0, 0, 0};
         }
     };
     auto compute = [&](const Frag &f) {
@@ -136,13 +169,118 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
             }
         }
     };
-    Frag f0, f1;
+    // PF register buffers of K blocks: the loads of PF-1 blocks are in flight
+    // while one is converted and multiplied (DYN: the first two are issued
+    // before the activation pass; a deeper prefetch measured slower).
+    constexpr int PF = 2;
+    Frag fr[PF];
+    Frag &f0 = fr[0], &f1 = fr[1];
+    // DYN: the activations as float4 groups i = r * kq + c (K % 16 == 0); UQ
+    // loads per thread are issued together, so one pass costs about one
+    // memory round trip per UQ * 512 groups.  The first round is issued ahead
+    // of the weight prefetch so that it returns from L2 without queueing
+    // behind the HBM loads.
+    constexpr int UQ = 8;
+    const uint32_t kq = (uint32_t)(g.K / 4);
+    const uint32_t nq = (uint32_t)g.M * kq;
+    auto xq = [&](uint32_t i) {
+        const uint32_t r = i / kq;
+        return reinterpret_cast<const f4 *>(g.x + (int64_t)r * g.ldx)[i - r * kq];
+    };
+    f4 v[UQ];
+    if constexpr (DYN) {
+#pragma unroll
+        for (int u = 0; u < UQ; ++u) {
+            const uint32_t i = u * NT + tid;
+            v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
     if (kb_begin < kb_end) load(f0, kb_begin);
-    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += 2 * UNROLL) {
-        if (kb0 + UNROLL < kb_end) load(f1, kb0 + UNROLL);
-        compute(f0);
-        if (kb0 + 2 * UNROLL < kb_end) load(f0, kb0 + 2 * UNROLL);
-        if (kb0 + UNROLL < kb_end) compute(f1);
+    float a_dyn = 1.0f;
+    if constexpr (DYN) {
+#pragma unroll
+        for (int p = 1; p < PF; ++p)
+            if (kb_begin + p * UNROLL < kb_end) load(fr[p], kb_begin + p * UNROLL);
+        __shared__ float wmax[WAVES];
+        float m = 0.0f;
+        for (uint32_t base = 0; base < nq; base += NT * UQ) {
+            if (base) {
+#pragma unroll
+                for (int u = 0; u < UQ; ++u) {
+                    const uint32_t i = base + u * NT + tid;
+                    v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UQ; ++u) {
+                // NaN compares false and is skipped, as in the standalone amax
+                const float ax = fabsf(v[u].x), ay = fabsf(v[u].y), az = fabsf(v[u].z), aw = fabsf(v[u].w);
+                m = ax > m ? ax : m; m = ay > m ? ay : m; m = az > m ? az : m; m = aw > m ? aw : m;
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            m = o > m ? o : m;
+        }
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+        m = wmax[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) m = wmax[w] > m ? wmax[w] : m;
+        a_dyn = scale_from_amax_bits(f32_bits(m));
+        if (g.scale_out && blockIdx.x == 0 && tid == 0) *g.scale_out = a_dyn;
+        const Recip d = make_recip(a_dyn);
+        auto put = [&](uint32_t i, f4 x4) {
+            const uint32_t r = i / kq;
+            reinterpret_cast<uint32_t *>(a_lds + r * pitch)[i - r * kq] = quantize4(x4.x, x4.y, x4.z, x4.w, d);
+        };
+        if (nq <= NT * UQ) {  // one round: the values are still in registers
+#pragma unroll
+            for (int u = 0; u < UQ; ++u) {
+                const uint32_t i = u * NT + tid;
+                if (i < nq) put(i, v[u]);
+            }
+        } else {
+            for (uint32_t base = 0; base < nq; base += NT * UQ) {
+#pragma unroll
+                for (int u = 0; u < UQ; ++u) {
+                    const uint32_t i = base + u * NT + tid;
+                    v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int u = 0; u < UQ; ++u) {
+                    const uint32_t i = base + u * NT + tid;
+                    if (i < nq) put(i, v[u]);
+                }
+            }
+        }
+        const uint32_t zq = (uint32_t)(pitch - 16) / 4 - kq;  // zero words per row for K <= k < Kp
+        for (uint32_t i = tid; i < (uint32_t)g.M * zq; i += NT) {
+            const uint32_t r = i / zq;
+            reinterpret_cast<uint32_t *>(a_lds + r * pitch)[kq + (i - r * zq)] = 0u;
+        }
+        __syncthreads();
+    }
+    if constexpr (DYN) {
+        // ring of PF register buffers: consume block kb, refill with kb + PF
+        for (int kb0 = kb_begin; kb0 < kb_end; kb0 += PF * UNROLL) {
+#pragma unroll
+            for (int p = 0; p < PF; ++p) {
+                const int kb = kb0 + p * UNROLL;
+                if (kb < kb_end) {
+                    read_a(fr[p], kb);
+                    compute(fr[p]);
+                    if (kb + PF * UNROLL < kb_end) load(fr[p], kb + PF * UNROLL);
+                }
+            }
+        }
+    } else {
+        for (int kb0 = kb_begin; kb0 < kb_end; kb0 += 2 * UNROLL) {
+            if (kb0 + UNROLL < kb_end) load(f1, kb0 + UNROLL);
+            compute(f0);
+            if (kb0 + 2 * UNROLL < kb_end) load(f0, kb0 + 2 * UNROLL);
+            if (kb0 + UNROLL < kb_end) compute(f1);
+        }
     }
 
 #pragma unroll
@@ -152,7 +290,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // 16 x 16*NB outputs: (block j, lane l, register r); MFMA output layout:
     // lane l holds column l%16 and rows (l/16)*4 + r.
     const Epilogue &e = g.e;
-    const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
+    const float a_s = DYN ? a_dyn : (e.a_scale ? e.a_scale[0] : 1.0f);
     for (int o = tid; o < NB * 256; o += NT) {
         const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
         const int64_t row = (l >> 4) * 4 + r;
@@ -176,12 +314,44 @@ hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a,
     g.nblk16 = Np / 16;
     g.nkb = (int)(Kp / 128);
     g.e = e;
+    g.x = nullptr; g.ldx = 0; g.scale_out = nullptr;
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
     unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
     if (exact)
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true>), dim3(grid), dim3(W * 64), 0, s, g);
+        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true, false>), dim3(grid), dim3(W * 64), 0, s, g);
     else
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, false>), dim3(grid), dim3(W * 64), 0, s, g);
+        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, false, false>), dim3(grid), dim3(W * 64), 0, s, g);
+    return hipGetLastError();
+}
+
+int64_t skinny_dynamic_lds_bytes(int64_t M, int64_t K) { return M * (pad_to(K, kPackK) + 16); }
+
+hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                                      const uint8_t *bp, const Epilogue &e, float *scale_out, bool exact,
+                                      hipStream_t s) {
+    SkinnyArgs g;
+    g.M = M; g.N = N; g.K = K; g.a = nullptr; g.lda = 0; g.bp = bp;
+    g.x = x; g.ldx = ldx; g.scale_out = scale_out;
+    int64_t Kp = pad_to(K, kPackK), Np = pad_to(N, kPanelCols);
+    g.KC = Kp / 16;
+    g.nblk16 = Np / 16;
+    g.nkb = (int)(Kp / 128);
+    g.e = e;
+    constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
+    const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
+    const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
+    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, true, true>)
+                           : reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, false, true>);
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[exact]) {
+        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kSkinnyDynLdsMax);
+        if (err != hipSuccess) return err;
+        attr_set[exact] = true;
+    }
+    if (exact)
+        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true, true>), dim3(grid), dim3(W * 64), lds, s, g);
+    else
+        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, false, true>), dim3(grid), dim3(W * 64), lds, s, g);
     return hipGetLastError();
 }
 

@@ -40,6 +40,76 @@ __host__ __device__ inline uint32_t e4m3_encode(float x) {
     return code == 0 ? s : (s | code);
 }
 
+// Two fp32 -> E4M3FN codes (a in bits 0-7, b in bits 8-15) through the
+// hardware conversion v_cvt_pk_fp8_f32 (round to nearest even into OCP
+// E4M3FN), with the reference encoder's special cases put around it:
+//   * clamping to +-448 first gives its saturation of |x| > 448 and of +-inf
+//     (every finite value above 448 encodes to 0x7e, as does 448 itself);
+//   * adding +0.0 turns -0.0 into +0.0 (the reference encodes both zeros as
+//     0x00, while a nonzero value that underflows keeps its sign: 0x80);
+//   * NaN is patched to 0x7f.
+// Equal to e4m3_encode on all 2^32 fp32 inputs (checked exhaustively on
+// gfx950 against the integer encoder above).
+__device__ inline uint32_t e4m3x2_hw(float a, float b) {
+    const float ca = __builtin_amdgcn_fmed3f(a + 0.0f, -448.0f, 448.0f);
+    const float cb = __builtin_amdgcn_fmed3f(b + 0.0f, -448.0f, 448.0f);
+    uint32_t v = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false) & 0xffffu;
+    if (a != a) v = (v & 0xff00u) | 0x7fu;
+    if (b != b) v = (v & 0x00ffu) | 0x7f00u;
+    return v;
+}
+
+// Division by a scale that is fixed for many elements, rounded exactly like
+// IEEE x / s.  With r = RN(1/s), q0 = RN(x*r) is within one ulp of x/s and
+// one Newton correction q = RN(q0 + RN(x - q0*s)*r) (the residual is exact
+// under fma) is the correctly rounded quotient (Markstein's theorem), as long
+// as nothing underflows.  Guards:
+//   * s outside [2^-60, 2^40] (1/s near the ends of the exponent range):
+//     plain IEEE division throughout;
+//   * 0 < |q0| < 2^-100 (the residual may be subnormal): IEEE division for
+//     that element; the quotient only decides between +-0 there;
+//   * q0 = +-inf (x/s beyond the fp32 range): q0 itself;
+//   * x = +-0 gives +0 (-0 / s would be -0; both encode to 0x00) and NaN
+//     stays NaN, which is all the encoder needs.
+// Checked on gfx950 against __fdiv_rn for 184 scales spread over the fast
+// range, each against all 2^32 fp32 x: every quotient with |q| >= 2^-11 (the
+// smallest magnitude the E4M3 encoding depends on) agrees bit for bit, and
+// all E4M3 encodings agree.
+struct Recip {
+    float s, r;
+    bool fast;
+};
+
+__device__ inline Recip make_recip(float s) {
+    Recip d;
+    d.s = s;
+    d.r = __fdiv_rn(1.0f, s);
+    d.fast = s >= 0x1p-60f && s <= 0x1p40f;
+    return d;
+}
+
+__device__ inline float div_by(float x, const Recip &d) {
+    if (!d.fast) return __fdiv_rn(x, d.s);
+    const float q0 = x * d.r;
+    float q = fmaf(fmaf(-q0, d.s, x), d.r, q0);
+    if (q0 != 0.0f && fabsf(q0) < 0x1p-100f) q = __fdiv_rn(x, d.s);
+    if (fabsf(q0) == __builtin_inff()) q = q0;
+    return q;
+}
+
+// dynamic per-tensor scale from the fp32 bits of amax = max |x| over the
+// non-NaN elements: amax / 448, or 1 when that is not a positive finite number
+__device__ inline float scale_from_amax_bits(uint32_t bits) {
+    float s = __fdiv_rn(bits_f32(bits), 448.0f);
+    if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
+    return s;
+}
+
+// four consecutive elements quantised with one scale -> four packed codes
+__device__ inline uint32_t quantize4(float a, float b, float c, float e, const Recip &d) {
+    return e4m3x2_hw(div_by(a, d), div_by(b, d)) | (e4m3x2_hw(div_by(c, d), div_by(e, d)) << 16);
+}
+
 // fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
 __host__ __device__ inline uint16_t bf16_rne(float f) {
     uint32_t u = f32_bits(f);

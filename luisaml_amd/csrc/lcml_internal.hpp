@@ -30,6 +30,13 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
                             const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
 hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                               const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
+// fused DynamicQuantizeLinear + skinny GEMM (fp32 activations, M <= 16):
+// LDS use is skinny_dynamic_lds_bytes(M, K) <= kSkinnyDynLdsMax
+constexpr int64_t kSkinnyDynLdsMax = 128 * 1024 - 32 * 1024;
+int64_t skinny_dynamic_lds_bytes(int64_t M, int64_t K);
+hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                                      const uint8_t *bp, const Epilogue &e, float *scale_out, bool exact,
+                                      hipStream_t s);
 hipError_t launch_gemv_valu_f32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda,
                                 const uint8_t *bp, const Epilogue &e, hipStream_t s);
 hipError_t launch_gemv_valu_fp8(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,

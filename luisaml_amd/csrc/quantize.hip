@@ -17,18 +17,10 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-__device__ inline uint32_t enc4(f4 v, float s) {
-    return e4m3_encode(__fdiv_rn(v.x, s)) | (e4m3_encode(__fdiv_rn(v.y, s)) << 8) |
-           (e4m3_encode(__fdiv_rn(v.z, s)) << 16) | (e4m3_encode(__fdiv_rn(v.w, s)) << 24);
-}
+// four elements of one per-tensor scale (reciprocal division + hardware
+// conversion, both exact stand-ins for the reference's x / s and encoder)
+__device__ inline uint32_t enc4(f4 v, const Recip &d) { return quantize4(v.x, v.y, v.z, v.w, d); }
 
-// Scale source: a float scale array indexed per axis, or the fp32 bits of a
-// reduced amax (dynamic per-tensor quantisation).
-__device__ inline float scale_from_amax_bits(uint32_t bits) {
-    float s = __fdiv_rn(bits_f32(bits), 448.0f);
-    if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
-    return s;
-}
 
 // Per-tensor (or per-axis with a 16-element-uniform scale index) vector path.
 // grid-stride over 16-element groups; requires x, y 16-byte aligned.
@@ -38,17 +30,18 @@ __global__ __launch_bounds__(kThreads) void k_quantize_vec(const float *__restri
                                                            int64_t axis_len, int64_t inner,
                                                            const float *__restrict__ scale,
                                                            const uint32_t *__restrict__ amax_bits) {
-    float s_tensor = 0.0f;
+    float s_tensor = 1.0f;
     if (FROM_AMAX) s_tensor = scale_from_amax_bits(*amax_bits);
     else if (axis_len == 1) s_tensor = scale[0];
+    const Recip d_tensor = make_recip(s_tensor);
     int64_t stride = (int64_t)gridDim.x * kThreads;
     for (int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x; g < ngroups; g += stride) {
-        float s = s_tensor;
-        if (!FROM_AMAX && axis_len != 1) s = scale[((g * kVec) / inner) % axis_len];
+        // per-axis: one scale per 16-element group (inner % 16 == 0)
+        const Recip d = (!FROM_AMAX && axis_len != 1) ? make_recip(scale[((g * kVec) / inner) % axis_len]) : d_tensor;
         const f4 *xp = reinterpret_cast<const f4 *>(x + g * kVec);
         f4 v0 = __builtin_nontemporal_load(xp + 0), v1 = __builtin_nontemporal_load(xp + 1);
         f4 v2 = __builtin_nontemporal_load(xp + 2), v3 = __builtin_nontemporal_load(xp + 3);
-        u4 out = {enc4(v0, s), enc4(v1, s), enc4(v2, s), enc4(v3, s)};
+        u4 out = {enc4(v0, d), enc4(v1, d), enc4(v2, d), enc4(v3, d)};
         *reinterpret_cast<u4 *>(y + g * kVec) = out;
     }
 }
@@ -213,11 +206,11 @@ __global__ __launch_bounds__(kRedThreads) void k_quantize_dynamic_spread(
         }
     }
     m = block_max<kRedThreads>(m, red);
-    float s = __fdiv_rn(m, 448.0f);
-    if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
+    const float s = scale_from_amax_bits(f32_bits(m));
+    const Recip d = make_recip(s);
     uint32_t *y4 = reinterpret_cast<uint32_t *>(y);
     for (int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kRedThreads)
-        y4[i] = enc4(x4[i], s);
+        y4[i] = enc4(x4[i], d);
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s;
 }
 
@@ -229,8 +222,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_quantize_dynamic_small(
     float m = 0.0f;
     for (int64_t i = threadIdx.x; i < n; i += kSmallThreads) m = absmax_acc(m, x[i]);
     m = block_max<kSmallThreads>(m, red);
-    float s = __fdiv_rn(m, 448.0f);
-    if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
+    const float s = scale_from_amax_bits(f32_bits(m));
     for (int64_t i = threadIdx.x; i < n; i += kSmallThreads) y[i] = (uint8_t)e4m3_encode(__fdiv_rn(x[i], s));
     if (threadIdx.x == 0) *scale_out = s;
 }

@@ -88,8 +88,8 @@ public:
 class FP8Linear : public StreamOperator {
     int a_mode_, has_c_, act_;
     float alpha_, beta_;
-    std::unique_ptr<DeviceBuffer> qa_, sa_, ws_;
-    size_t qa_bytes_ = 0;
+    std::unique_ptr<DeviceBuffer> qa_, ws_;
+    size_t qa_bytes_ = 0, ws_bytes_ = 0;
 
 public:
     FP8Linear(int a_mode, int has_c, int act, float alpha, float beta)
@@ -116,6 +116,20 @@ public:
                   "FP8Linear");
             return;
         }
+        if (a_mode_ == 2) {
+            // DynamicQuantizeLinear -> DQ -> Gemm in one call (one fused launch
+            // for small M*K; otherwise quantise into the workspace + GEMM)
+            const int64_t ws = lcml_fp8_gemm_dynamic_workspace_bytes(M, K, LCML_KERNEL_AUTO);
+            if (ws > 0 && (!ws_ || ws_bytes_ < (size_t)ws)) {
+                ws_ = std::make_unique<DeviceBuffer>((size_t)ws);
+                ws_bytes_ = (size_t)ws;
+            }
+            check(lcml_fp8_gemm_dynamic(M, N, K, a, K, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
+                                        c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, nullptr,
+                                        ws > 0 ? ws_->data() : nullptr, ws, LCML_KERNEL_AUTO, stream_),
+                  "FP8Linear");
+            return;
+        }
         // quantised activation scratch: M*K E4M3 bytes (16-byte aligned rows need K % 16 == 0)
         const size_t need = (size_t)(M * K);
         if (!qa_ || qa_bytes_ < need) {
@@ -123,17 +137,8 @@ public:
             qa_bytes_ = need;
         }
         uint8_t *q = static_cast<uint8_t *>(qa_->data());
-        const float *sa;
-        if (a_mode_ == 1) {
-            sa = static_cast<const float *>(a_scale->device_data());
-            check(lcml_fp8_quantize(a, q, 1, 1, M * K, sa, stream_), "FP8Linear quantize");
-        } else {
-            if (!sa_) sa_ = std::make_unique<DeviceBuffer>(sizeof(float));
-            if (!ws_) ws_ = std::make_unique<DeviceBuffer>(LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
-            check(lcml_fp8_quantize_dynamic(a, q, M * K, static_cast<float *>(sa_->data()), ws_->data(), stream_),
-                  "FP8Linear quantize");
-            sa = static_cast<const float *>(sa_->data());
-        }
+        const float *sa = static_cast<const float *>(a_scale->device_data());
+        check(lcml_fp8_quantize(a, q, 1, 1, M * K, sa, stream_), "FP8Linear quantize");
         check(lcml_fp8_gemm(M, N, K, q, K, sa, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim, c.d0,
                             c.d1, beta_, act_, Y.device_data(), ydt, N, LCML_KERNEL_AUTO, stream_),
               "FP8Linear");
