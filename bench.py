@@ -54,6 +54,12 @@ def gemm_kernel_bytes(M: int) -> int:
     return SMALL_K * SMALL_N + 4 * SMALL_N + M * SMALL_K + 2 * M * SMALL_N
 
 
+def oracle_free_dynamic_scale(w: np.ndarray) -> np.float32:
+    """Per-tensor E4M3 scale amax/448 (1.0 when not a positive finite number)."""
+    s = np.float32(np.max(np.abs(np.nan_to_num(w, nan=0.0)))) / np.float32(448.0)
+    return np.float32(s) if (s > 0 and np.isfinite(s)) else np.float32(1.0)
+
+
 def cpu_threads() -> int:
     try:
         n = len(os.sched_getaffinity(0))
@@ -245,6 +251,134 @@ def main() -> int:
                                          "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                                          "frac": round(big["exact_bf16_mfma"]["tflops"] / FP8_PEAK_TFLOPS, 4)}}
         del qa, bp, y
+
+    # ------------------------------------------ transformer-block linears ---
+    if not args.no_big:
+        # batch 8 x seq 512 (M = 4096), hidden 4096: QKV 4096->12288, O 4096->4096,
+        # up 4096->11008 + GELU (fp32 out), down 11008->4096 on the GELU output;
+        # every linear quantises its fp32 input per tensor (dynamic scale) and
+        # adds an fp32 bias; weights N(0,0.02) with per-channel E4M3 scales.
+        # The attention core is not part of this path: O-proj reads x.
+        Mt, H = 4096, 4096
+        shapes = {"qkv": (H, 3 * H), "o": (H, H), "up": (H, 11008), "down": (11008, H)}
+        wts = {}
+        for i, (name, (kk, nn)) in enumerate(shapes.items()):
+            wf = torch.from_numpy(synth.normal(400 + i, (kk, nn), std=0.02)).to(dev)
+            sc = torch.from_numpy(channel_scales_np(wf.cpu().numpy(), axis=0)).to(dev)
+            wts[name] = (capi.pack_weight(capi.quantize(wf, sc, axis=1), w_is_nk=False), sc,
+                         torch.from_numpy(synth.normal(410 + i, (nn,), std=0.01)).to(dev))
+            del wf
+        xt = torch.from_numpy(synth.normal(420, (Mt, H))).to(dev)
+        y_qkv = torch.empty((Mt, 3 * H), dtype=torch.bfloat16, device=dev)
+        y_o = torch.empty((Mt, H), dtype=torch.bfloat16, device=dev)
+        y_up = torch.empty((Mt, 11008), dtype=torch.float32, device=dev)
+        y_dn = torch.empty((Mt, H), dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(capi.lib().lcml_fp8_gemm_dynamic_workspace_bytes(Mt, 11008, capi.KERNEL_MFMA),
+                         dtype=torch.uint8, device=dev)
+        flops_block = 2.0 * Mt * sum(kk * nn for kk, nn in shapes.values())
+
+        def block(kern):
+            def lin(x_in, name, y, act=capi.ACT_NONE):
+                bp_, sc_, b_ = wts[name]
+                kk, nn = shapes[name]
+                capi.gemm_dynamic(x_in, bp_, sc_, nn, kk, c=b_, act=act, out=y, kernel=kern, workspace=ws)
+            lin(xt, "qkv", y_qkv)
+            lin(xt, "o", y_o)
+            lin(xt, "up", y_up, act=capi.ACT_GELU_ERF)
+            lin(y_up, "down", y_dn)
+
+        blk = {}
+        for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
+                                 ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
+            block(kern)
+            n = max(2, args.steps // 4)
+            ms = timed(lambda: [block(kern) for _ in range(n)]) / n
+            tf = flops_block / (ms * 1e-3) / 1e12
+            blk[name] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+                         "pct_fp8_peak": round(100 * tf / FP8_PEAK_TFLOPS, 1),
+                         "pct_instruction_peak": round(100 * tf / peak, 1)}
+        out["transformer_linears_m4096"] = {
+            "workload": "M=4096 (batch 8 x seq 512), hidden 4096: QKV 4096->12288, O 4096->4096, up 4096->11008 "
+                        "+GELU, down 11008->4096; each linear = dynamic per-tensor quantize of its fp32 input + "
+                        "FP8 GEMM with per-channel scales + fp32 bias (GELU on up); bf16 outputs except up (fp32, "
+                        "re-quantised by down)", "flops": flops_block, **blk}
+        del wts, xt, y_qkv, y_o, y_up, y_dn, ws
+
+    # ------------------------------------------------------- conv as GEMM ---
+    if not args.no_big:
+        # ResNet-style 3x3 conv: x[32,256,56,56] fp32 N(0,1), dynamic per-tensor
+        # E4M3 (written NHWC), W[256,256,3,3] N(0,0.03) per-output-channel
+        # E4M3, stride 1, pad 1, bias + ReLU, NCHW fp32 out; the GEMM view is
+        # M = 100352, K = 2304, N = 256 with the im2col done in the A loads
+        cn, cc, ch, cw, cco = 32, 256, 56, 56, 256
+        xc = torch.from_numpy(synth.normal(600, (cn, cc, ch, cw))).to(dev)
+        wc = synth.normal(601, (cco, cc, 3, 3), std=0.03)
+        wsc = channel_scales_np(wc.reshape(cco, -1), axis=1)
+        d_wsc = torch.from_numpy(wsc).to(dev)
+        qwc = capi.quantize(torch.from_numpy(wc.reshape(cco, -1)).to(dev), d_wsc, axis=0).reshape(cco, cc, 3, 3)
+        bpc = capi.pack_conv_weight(qwc.contiguous())
+        bc = torch.from_numpy(synth.normal(602, (cco,), std=0.01)).to(dev)
+        xq = torch.empty((cn, ch, cw, cc), dtype=torch.uint8, device=dev)
+        sxc = torch.empty(1, dtype=torch.float32, device=dev)
+        wsq = torch.empty(256, dtype=torch.uint8, device=dev)
+        yc = torch.empty((cn, cco, ch, cw), dtype=torch.float32, device=dev)
+        conv_flops = 2.0 * cn * ch * cw * cco * cc * 9
+        conv = {}
+
+        def quant_c():
+            capi.quantize_nhwc(xc, out=xq, scale_out=sxc, workspace=wsq)
+
+        quant_c()
+        n = max(3, args.steps // 2)
+        q_ms = timed(lambda: [quant_c() for _ in range(n)]) / n
+        for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
+                                 ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
+            def conv_c():
+                capi.conv2d(xq, sxc, bpc, d_wsc, cco, (3, 3), pads=(1, 1), bias=bc, act=capi.ACT_RELU, out=yc,
+                            kernel=kern)
+            conv_c()
+            ms = timed(lambda: [conv_c() for _ in range(n)]) / n
+            tf = conv_flops / (ms * 1e-3) / 1e12
+            conv[name] = {"conv_ms": round(ms, 4), "tflops": round(tf, 1),
+                          "pct_fp8_peak": round(100 * tf / FP8_PEAK_TFLOPS, 1),
+                          "pct_instruction_peak": round(100 * tf / peak, 1),
+                          "with_quantize_ms": round(ms + q_ms, 4)}
+        in_bytes = cn * cc * ch * cw * 4
+        out["conv3x3_resnet"] = {
+            "workload": "x[32,256,56,56] fp32 -> dynamic E4M3 (NHWC) -> 3x3 conv pad 1 (implicit im2col GEMM "
+                        "M=100352 K=2304 N=256, per-channel E4M3 weights) + bias + ReLU -> NCHW fp32",
+            "flops": conv_flops, "quantize_nhwc_ms": round(q_ms, 4),
+            "quantize_nhwc_gbs": round((in_bytes + in_bytes // 4) / (q_ms * 1e-3) / 1e9, 1), **conv}
+        del xc, xq, yc, bpc
+
+    # ---------------------------------------------------------- 3-layer MLP ---
+    # 784->256 (+ReLU) -> 128 (+ReLU) -> 10, batch 64, fp32 activations, E4M3
+    # weights with one per-tensor scale each through DequantizeLinear (W8A32)
+    mlp = []
+    for i, (kk, nn) in enumerate(((784, 256), (256, 128), (128, 10))):
+        wf = synth.normal(500 + i, (nn, kk), std=0.05)  # Gemm transB=1 layout
+        sc = np.array([oracle_free_dynamic_scale(wf)], np.float32)
+        d_sc = torch.from_numpy(sc).to(dev)
+        q = capi.quantize(torch.from_numpy(wf).to(dev), d_sc)
+        mlp.append((capi.pack_weight(q, w_is_nk=True), d_sc, torch.from_numpy(synth.normal(510 + i, (nn,), std=0.01))
+                    .to(dev), kk, nn))
+    x_mlp = torch.from_numpy(synth.uniform(520, (64, 784))).to(dev)
+    bufs = [torch.empty((64, nn), dtype=torch.float32, device=dev) for (_, _, _, _, nn) in mlp]
+
+    def mlp_fwd(_i=0):
+        h = x_mlp
+        for j, (bp_, sc_, b_, kk, nn) in enumerate(mlp):
+            capi.gemm_w8a32(h, bp_, sc_, nn, kk, c=b_, act=capi.ACT_RELU if j < 2 else capi.ACT_NONE, out=bufs[j])
+            h = bufs[j]
+
+    mlp_fwd()
+    g_mlp = capture(mlp_fwd, 50)
+    g_mlp.replay()
+    mlp_us = 1e3 * timed(g_mlp.replay) / 50
+    out["mlp_784_256_128_10"] = {"workload": "3-layer MLP batch 64, W8A32 (DequantizeLinear weights, fp32 "
+                                             "activations), bias + ReLU fused, HIP-graph replay",
+                                 "us_per_forward": round(mlp_us, 2), "flops": 2 * 64 * (784 * 256 + 256 * 128 + 128 * 10)}
+    del g_mlp
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)

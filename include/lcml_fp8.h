@@ -189,6 +189,52 @@ LCML_API int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float 
                           void *workspace, int64_t workspace_bytes, int kernel, void *stream);
 
 /*
+ * QuantizeLinear of an NCHW fp32 activation [n, c, h, w] with one per-tensor
+ * scale, written in NHWC order (y[n][h][w][c], E4M3) for lcml_fp8_conv2d.
+ * y_scale: device float; NULL selects the dynamic scale amax/448 (1 when
+ *   that is not a positive finite number), written to scale_out (required)
+ *   and computed with `workspace` (LCML_FP8_DYNAMIC_WORKSPACE_BYTES).
+ * c % 4 == 0.  Same codes as lcml_fp8_quantize on the same values (the
+ * reference encoder of fp_quantized.h:149-223 on x / scale); only the order
+ * of the output bytes differs.
+ */
+LCML_API int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64_t c, int64_t h, int64_t w,
+                           const float *y_scale, float *scale_out, void *workspace, void *stream);
+
+/*
+ * Conv weights: E4M3 [cout][cin][kh][kw] (ONNX Conv W layout, dense) packed
+ * for lcml_fp8_conv2d: the GEMM weight with reduction index
+ * k = (kh*KW + kw)*cin + c (the reference Conv's loop order kh, kw, then
+ * channels, src/onnx/operators/conv.cpp:143-192) and columns = cout, in the
+ * lcml_fp8_pack_weight panel layout.  Size:
+ * lcml_fp8_packed_weight_bytes(kh*kw*cin, cout).
+ */
+LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin, int64_t kh, int64_t kw,
+                              uint8_t *packed, void *stream);
+
+/*
+ * 2-D convolution with E4M3 input and weights, fp32 accumulation, as an
+ * implicit-im2col GEMM on the matrix cores (no im2col buffer):
+ *   y[n][co][oh][ow] = act( x_scale * w_scale[co|0] *
+ *        sum_{kh,kw,c} x[n][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw][c] * w[co][c][kh][kw]
+ *        + bias[co] )
+ * with out-of-range input positions contributing zero.  pad_h/pad_w are the
+ * BEGIN pads (the reference applies only those, conv.cpp:121; end pads only
+ * enter through the output size oh x ow, which the caller passes).
+ * x_nhwc: lcml_fp8_quantize_nhwc output; c % 16 == 0; group must be 1.
+ * w_packed: lcml_fp8_pack_conv_weight output.  bias: cout floats or NULL.
+ * y: NCHW [n][cout][oh][ow], y_dtype LCML_DTYPE_FLOAT or BFLOAT16.
+ * kernel: LCML_KERNEL_AUTO / MFMA (exact bf16 matrix cores) or MFMA_FP8.
+ * Replaces Conv::apply (src/onnx/operators/conv.cpp:115-207) for the
+ * DQ(x), DQ(W) -> Conv [-> Relu] pattern.
+ */
+LCML_API int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int64_t c, int64_t h,
+                    int64_t w, const uint8_t *w_packed, const float *w_scale, int w_scale_per_channel,
+                    int64_t cout, int64_t kh, int64_t kw, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                    int64_t pad_w, int64_t dil_h, int64_t dil_w, int64_t group, int64_t oh, int64_t ow,
+                    const float *bias, int act, void *y, int y_dtype, int kernel, void *stream);
+
+/*
  * W8A32 linear: fp32 activations times packed E4M3 weights, same epilogue:
  *   y[m,n] = act( alpha * (sum_k a[m,k] * to_float(B[k,n])) * b_scale[n|0]
  *                 + beta * C )

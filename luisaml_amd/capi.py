@@ -49,6 +49,10 @@ _SIGS = {
     "lcml_fp8_gemm_dynamic_workspace_bytes": (_i64, [_i64, _i64, _int]),
     "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
                                      _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
+    "lcml_fp8_quantize_nhwc": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "lcml_fp8_pack_conv_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "lcml_fp8_conv2d": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _vp]),
     "lcml_fp8_gemm_w8a32": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int,
                                    _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
     "lcml_fp8_sgemm": (_int, [_i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _f32, _vp, _int, _i64,
@@ -236,6 +240,55 @@ def gemm_dynamic(x: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor,
                                        float(alpha), _ptr(cc), nd, c0, c1, float(beta), int(act), _ptr(y), ydt,
                                        y.stride(0), _ptr(scale_out), _ptr(workspace), ws_bytes, int(kernel),
                                        _stream(stream)))
+    return y
+
+
+# --------------------------------------------------------------- Conv -------
+
+def quantize_nhwc(x: torch.Tensor, scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                  scale_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, stream=None):
+    """QuantizeLinear of NCHW fp32 x into NHWC E4M3; scale None = dynamic.
+    Returns (codes [n, h, w, c], scale[1])."""
+    assert x.dtype == torch.float32 and x.is_contiguous() and x.dim() == 4
+    n, c, h, w = x.shape
+    y = out if out is not None else torch.empty((n, h, w, c), dtype=torch.uint8, device=x.device)
+    if scale is None:
+        s = scale_out if scale_out is not None else torch.empty(1, dtype=torch.float32, device=x.device)
+        ws = workspace if workspace is not None else torch.empty(DYNAMIC_WORKSPACE_BYTES, dtype=torch.uint8,
+                                                                 device=x.device)
+        _check(lib().lcml_fp8_quantize_nhwc(_ptr(x), _ptr(y), n, c, h, w, None, _ptr(s), _ptr(ws), _stream(stream)))
+        return y, s
+    _check(lib().lcml_fp8_quantize_nhwc(_ptr(x), _ptr(y), n, c, h, w, _ptr(scale), None, None, _stream(stream)))
+    return y, scale
+
+
+def pack_conv_weight(w: torch.Tensor, stream=None) -> torch.Tensor:
+    """Pack E4M3 conv weights [cout, cin, kh, kw] for conv2d."""
+    assert w.dtype == torch.uint8 and w.is_contiguous() and w.dim() == 4
+    cout, cin, kh, kw = w.shape
+    p = torch.empty(packed_weight_bytes(kh * kw * cin, cout), dtype=torch.uint8, device=w.device)
+    _check(lib().lcml_fp8_pack_conv_weight(_ptr(w), cout, cin, kh, kw, _ptr(p), _stream(stream)))
+    return p
+
+
+def conv2d(x_nhwc: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+           cout: int, kernel_shape, strides=(1, 1), pads=(0, 0), dilations=(1, 1), out_hw=None,
+           bias: torch.Tensor | None = None, act: int = ACT_NONE, out_dtype=torch.float32,
+           kernel: int = KERNEL_AUTO, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """FP8 conv (implicit im2col on the matrix cores): NHWC E4M3 in, NCHW out.
+    pads are begin pads; out_hw defaults to symmetric padding."""
+    n, h, w, c = x_nhwc.shape
+    kh, kw = kernel_shape
+    if out_hw is None:
+        out_hw = ((h + 2 * pads[0] - dilations[0] * (kh - 1) - 1) // strides[0] + 1,
+                  (w + 2 * pads[1] - dilations[1] * (kw - 1) - 1) // strides[1] + 1)
+    oh, ow = out_hw
+    y = out if out is not None else torch.empty((n, cout, oh, ow), dtype=out_dtype, device=x_nhwc.device)
+    per_ch = int(w_scale.numel() > 1)
+    _check(lib().lcml_fp8_conv2d(_ptr(x_nhwc), _ptr(x_scale), n, c, h, w, _ptr(w_packed), _ptr(w_scale), per_ch,
+                                 cout, kh, kw, strides[0], strides[1], pads[0], pads[1], dilations[0], dilations[1],
+                                 1, oh, ow, _ptr(bias), int(act), _ptr(y), _DTYPE_CODE.get(y.dtype, 0), int(kernel),
+                                 _stream(stream)))
     return y
 
 

@@ -245,6 +245,74 @@ int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64
                          c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
 }
 
+int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64_t c, int64_t h, int64_t w,
+                           const float *y_scale, float *scale_out, void *workspace, void *stream) {
+    const char *fn = "lcml_fp8_quantize_nhwc";
+    if (n < 0 || c <= 0 || h <= 0 || w <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: bad shape", fn);
+    if (c % 4 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: c=%lld is not a multiple of 4", fn, (long long)c);
+    if (n * c * h * w >= (int64_t)1 << 31 || n * h >= ((int64_t)1 << 31))
+        return fail(LCML_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+    if (n == 0) return LCML_OK;
+    if (!x || !y) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (!aligned(y, 4)) return fail(LCML_ERR_INVALID_ARG, "%s: y must be 4-byte aligned", fn);
+    hipStream_t s = (hipStream_t)stream;
+    if (y_scale)
+        return hip_status(lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, y_scale, nullptr, nullptr, s),
+                          fn);
+    if (!scale_out || !workspace)
+        return fail(LCML_ERR_INVALID_ARG, "%s: the dynamic scale needs scale_out and a workspace", fn);
+    uint32_t *word = static_cast<uint32_t *>(workspace);
+    hipError_t err = lcml::launch_fill_u32(word, 0u, 1, s);
+    if (err == hipSuccess) err = lcml::launch_amax(x, n * c * h * w, word, s);
+    if (err == hipSuccess) err = lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, nullptr, word, scale_out, s);
+    return hip_status(err, fn);
+}
+
+int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin, int64_t kh, int64_t kw, uint8_t *packed,
+                              void *stream) {
+    const char *fn = "lcml_fp8_pack_conv_weight";
+    if (cout <= 0 || cin <= 0 || kh <= 0 || kw <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: bad shape", fn);
+    if (!w || !packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (!aligned(packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: packed not 16-byte aligned", fn);
+    return hip_status(lcml::launch_pack_conv_weight(w, (int)cout, (int)cin, (int)kh, (int)kw, packed,
+                                                    (hipStream_t)stream),
+                      fn);
+}
+
+int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int64_t c, int64_t h, int64_t w,
+                    const uint8_t *w_packed, const float *w_scale, int w_scale_per_channel, int64_t cout, int64_t kh,
+                    int64_t kw, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h,
+                    int64_t dil_w, int64_t group, int64_t oh, int64_t ow, const float *bias, int act, void *y,
+                    int y_dtype, int kernel, void *stream) {
+    const char *fn = "lcml_fp8_conv2d";
+    if (n < 0 || c <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0 || oh <= 0 || ow <= 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: bad shape", fn);
+    if (stride_h <= 0 || stride_w <= 0 || dil_h <= 0 || dil_w <= 0 || pad_h < 0 || pad_w < 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: strides and dilations must be >= 1, pads >= 0", fn);
+    if (group != 1) return fail(LCML_ERR_UNSUPPORTED, "%s: group=%lld (only 1 is implemented)", fn, (long long)group);
+    if (c % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: c=%lld is not a multiple of 16", fn, (long long)c);
+    const int64_t M = n * oh * ow, K = kh * kw * c;
+    if (n * h * w * c >= (int64_t)1 << 31 || M >= (int64_t)1 << 31 ||
+        lcml_fp8_packed_weight_bytes(K, cout) >= (int64_t)1 << 31)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB", fn);
+    if (kernel == LCML_KERNEL_AUTO) kernel = LCML_KERNEL_MFMA;
+    if (kernel != LCML_KERNEL_MFMA && kernel != LCML_KERNEL_MFMA_FP8)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: kernel %d (AUTO, MFMA or MFMA_FP8)", fn, kernel);
+    lcml::Epilogue e;
+    if (int rc = make_epilogue(e, fn, M, cout, x_scale, w_scale, w_scale_per_channel, 1.0f, bias, 1, cout, 0, 1.0f,
+                               act, y, y_dtype, cout))
+        return rc;
+    if (n == 0) return LCML_OK;
+    if (!x_nhwc || !w_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (!aligned(x_nhwc, 16) || !aligned(w_packed, 16))
+        return fail(LCML_ERR_INVALID_ARG, "%s: x_nhwc and w_packed must be 16-byte aligned", fn);
+    return hip_status(lcml::launch_conv_mfma(x_nhwc, n, (int)c, (int)h, (int)w, w_packed, (int)cout, (int)kh, (int)kw,
+                                             (int)stride_h, (int)stride_w, (int)pad_h, (int)pad_w, (int)dil_h,
+                                             (int)dil_w, (int)oh, (int)ow, e, kernel == LCML_KERNEL_MFMA,
+                                             (hipStream_t)stream),
+                      fn);
+}
+
 int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, const uint8_t *b_packed,
                         const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
                         int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,

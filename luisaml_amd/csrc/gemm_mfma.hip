@@ -73,7 +73,20 @@ struct Tile {
     static_assert(BM % 64 == 0 && BN % 64 == 0 && (BM / 8) % NW == 0 && (BN / 8) % NW == 0, "tile shape");
 };
 
+// Implicit-im2col convolution geometry (CONV instantiation).  A is the
+// quantised input in NHWC order, so the GEMM row m = (n, oh, ow) and the
+// reduction index k = (kh, kw, c) — the reference's loop order (kh, kw, then
+// channels, conv.cpp:143-192) — address the bytes
+//   X[n][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw][c]
+// and taps that fall into the padding read zeros (the reference's unsigned
+// bounds check, conv.cpp:145-148; begin pads only, conv.cpp:121).  The
+// output goes to NCHW: Y[n][co][oh][ow].
+struct ConvGeom {
+    int H, W, C, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw;
+};
+
 struct GemmArgs {
+    ConvGeom cv;
     int64_t M, N, K;
     const uint8_t *a;
     int64_t lda;
@@ -98,7 +111,7 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 
 __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT>
+template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV>
 __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs g) {
     using T = Tile<WAVES_M, WAVES_N, WM, WN>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -126,12 +139,26 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
     uint32_t a_off[T::A_BLK];
     int a_kc[T::A_BLK];
     uint32_t b_off[T::B_BLK];
+    int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
 #pragma unroll
     for (int i = 0; i < T::A_BLK; ++i) {
         const int r = (wave * T::A_BLK + i) * 8 + (lane >> 3);
         const int c = (lane & 7) ^ ((r >> 1) & 7);
         a_kc[i] = c * 16;
-        a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
+        if constexpr (CONV) {
+            // a_off = the row's image base n*H*W*C; rows past M get an input
+            // pixel that is out of range for every tap
+            const ConvGeom &cv = g.cv;
+            const int64_t m = m0 + r;
+            const uint32_t ohw = (uint32_t)(cv.OH * cv.OW);
+            const uint32_t mm = m < g.M ? (uint32_t)m : 0u;
+            const uint32_t n = mm / ohw, pix = mm - n * ohw, oh = pix / (uint32_t)cv.OW, ow = pix - oh * (uint32_t)cv.OW;
+            a_off[i] = n * (uint32_t)(cv.H * cv.W * cv.C);
+            a_ih0[i] = m < g.M ? (int)oh * cv.sh - cv.ph : -(1 << 30);
+            a_iw0[i] = (int)ow * cv.sw - cv.pw;
+        } else {
+            a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
+        }
     }
 #pragma unroll
     for (int i = 0; i < T::B_BLK; ++i) {
@@ -144,8 +171,20 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
         const uint32_t kbyte = (uint32_t)kt * BK;
 #pragma unroll
         for (int i = 0; i < T::A_BLK; ++i) {
-            const uint32_t off =
-                (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
+            uint32_t off;
+            if constexpr (CONV) {
+                // k -> (tap, channel) -> (kh, kw); C % 16 == 0 keeps every
+                // 16-byte chunk inside one tap
+                const ConvGeom &cv = g.cv;
+                const uint32_t k = kbyte + (uint32_t)a_kc[i];
+                const uint32_t tap = k / (uint32_t)cv.C, cin = k - tap * (uint32_t)cv.C;
+                const uint32_t kh = tap / (uint32_t)cv.KW, kw = tap - kh * (uint32_t)cv.KW;
+                const int ih = a_ih0[i] + (int)kh * cv.dh, iw = a_iw0[i] + (int)kw * cv.dw;
+                const bool ok = (int64_t)k < g.K && (uint32_t)ih < (uint32_t)cv.H && (uint32_t)iw < (uint32_t)cv.W;
+                off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.C + cin : OOB;
+            } else {
+                off = (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
+            }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * T::A_BLK + i) * 1024), 16,
                                                      off, 0, 0, 0);
         }
@@ -244,15 +283,41 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
             for (int r = 0; r < 16; ++r)
                 st[(i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EP_PITCH + (lane & 31)] = acc[i][j][r];
         __syncthreads();
-        const int64_t col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
-        if (col < e.N) {
-            const float sc = epi_scale(e, a_s, col);
-            const int64_t row0 = m0 + wm * WM * 32 + (lane >> 5);
+        if constexpr (CONV) {
+            // NCHW output: lanes run along output pixels (rows), so each
+            // column's stores are contiguous
+            const uint32_t ohw = (uint32_t)(g.cv.OH * g.cv.OW);
+#pragma unroll
+            for (int h = 0; h < WM / 2; ++h) {
+                const int rl = h * 64 + lane;
+                const int64_t m = m0 + wm * WM * 32 + rl;
+                if (m < e.M) {
+                    const uint32_t n = (uint32_t)m / ohw, pix = (uint32_t)m - n * ohw;
+                    const int64_t ybase = (int64_t)n * e.N * ohw + pix;
 #pragma unroll 1
-            for (int q = 0; q < WM * 16; ++q) {
-                const int64_t row = row0 + 2 * q;
-                if (row >= e.M) break;
-                epi_store(e, row, col, epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
+                    for (int c = 0; c < 32; ++c) {
+                        const int64_t col = n0 + wn * WN * 32 + j * 32 + c;
+                        if (col >= e.N) break;
+                        const float v = epi_value(e, epi_scale(e, a_s, col), m, col, st[rl * EP_PITCH + c]);
+                        if (e.y_bf16)
+                            reinterpret_cast<uint16_t *>(e.y)[ybase + col * ohw] = bf16_rne(v);
+                        else
+                            reinterpret_cast<float *>(e.y)[ybase + col * ohw] = v;
+                    }
+                }
+            }
+        } else {
+            const int64_t col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
+            if (col < e.N) {
+                const float sc = epi_scale(e, a_s, col);
+                const int64_t row0 = m0 + wm * WM * 32 + (lane >> 5);
+#pragma unroll 1
+                for (int q = 0; q < WM * 16; ++q) {
+                    const int64_t row = row0 + 2 * q;
+                    if (row >= e.M) break;
+                    epi_store(e, row, col,
+                              epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
+                }
             }
         }
         __syncthreads();
@@ -261,38 +326,51 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
 
 constexpr int WAVES_M = LCML_GEMM_WAVES_M, WAVES_N = LCML_GEMM_WAVES_N;
 constexpr int WM = 256 / 32 / WAVES_M, WN = 256 / 32 / WAVES_N;
+static_assert(WM % 2 == 0, "the NCHW epilogue walks 64-row halves");
 using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
-bool g_attr_set[2] = {false, false};
+
+template <bool EXACT, bool CONV>
+hipError_t launch(GemmArgs &g, hipStream_t s) {
+    auto *fn = k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, EXACT, CONV>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, Shipped::LDS_BYTES);
+        if (err != hipSuccess) return err;
+        attr_set = true;
+    }
+    int64_t Kp = pad_to(g.K, kPackK), Np = pad_to(g.N, kPanelCols);
+    g.KC = Kp / 16;
+    g.npanels = Np / 64;
+    g.tiles_m = (int)((g.M + Shipped::BM - 1) / Shipped::BM);
+    g.tiles_n = (int)((g.N + Shipped::BN - 1) / Shipped::BN);
+    g.nk = (int)(Kp / BK);
+    g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
+    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n), dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
+    return hipGetLastError();
+}
 
 }  // namespace
 
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                             const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
-    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, true>)
-                           : reinterpret_cast<const void *>(k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, false>);
-    if (!g_attr_set[exact]) {
-        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Shipped::LDS_BYTES);
-        if (err != hipSuccess) return err;
-        g_attr_set[exact] = true;
-    }
-    GemmArgs g;
+    GemmArgs g = {};
     g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
-    int64_t Kp = pad_to(K, kPackK), Np = pad_to(N, kPanelCols);
-    g.KC = Kp / 16;
-    g.npanels = Np / 64;
-    g.tiles_m = (int)((M + Shipped::BM - 1) / Shipped::BM);
-    g.tiles_n = (int)((N + Shipped::BN - 1) / Shipped::BN);
-    g.nk = (int)(Kp / BK);
     g.a_bytes = (uint32_t)((M - 1) * lda + K);
-    g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
     g.e = e;
-    if (exact)
-        hipLaunchKernelGGL((k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, true>), dim3(g.tiles_m * g.tiles_n),
-                           dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
-    else
-        hipLaunchKernelGGL((k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, false>), dim3(g.tiles_m * g.tiles_n),
-                           dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
-    return hipGetLastError();
+    return exact ? launch<true, false>(g, s) : launch<false, false>(g, s);
+}
+
+hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
+                            int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int OH, int OW,
+                            const Epilogue &e, bool exact, hipStream_t s) {
+    GemmArgs g = {};
+    g.cv = ConvGeom{H, W, C, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw};
+    g.M = Nb * OH * OW; g.N = Cout; g.K = (int64_t)KH * KW * C;
+    g.a = x_nhwc; g.lda = 0; g.bp = bp;
+    g.a_bytes = (uint32_t)(Nb * H * W * C);
+    g.e = e;
+    return exact ? launch<true, true>(g, s) : launch<false, true>(g, s);
 }
 
 }  // namespace lcml
