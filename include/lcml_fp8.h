@@ -256,6 +256,18 @@ LCML_API int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a
  * a: [M,K] (or [K,M] when trans_a) with row pitch lda; b: [K,N] (or [N,K]
  * when trans_b) with row pitch ldb; C and y as in lcml_fp8_gemm.
  */
+/*
+ * Plain fp32 2-D convolution for graphs that stay in fp32 (the reference
+ * Conv::apply, src/onnx/operators/conv.cpp:115-207): x NCHW, w
+ * [cout][c/group][kh][kw], bias (cout floats or NULL), y NCHW fp32
+ * [n][cout][oh][ow]; begin pads, strides, dilations, groups; one sequential
+ * fma chain per output over (kh, kw, channel).
+ */
+LCML_API int lcml_fp8_conv2d_f32(const float *x, const float *w, const float *bias, float *y, int64_t n, int64_t c,
+                        int64_t h, int64_t wd, int64_t cout, int64_t kh, int64_t kw, int64_t stride_h,
+                        int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h, int64_t dil_w,
+                        int64_t group, int64_t oh, int64_t ow, int act, void *stream);
+
 LCML_API int lcml_fp8_sgemm(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, int trans_a,
                             const float *b, int64_t ldb, int trans_b, float alpha, const float *c, int c_ndim,
                             int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype,

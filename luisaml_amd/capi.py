@@ -53,6 +53,8 @@ _SIGS = {
     "lcml_fp8_pack_conv_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "lcml_fp8_conv2d": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _vp]),
+    "lcml_fp8_conv2d_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "lcml_fp8_gemm_w8a32": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int,
                                    _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
     "lcml_fp8_sgemm": (_int, [_i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _f32, _vp, _int, _i64,
@@ -289,6 +291,22 @@ def conv2d(x_nhwc: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, 
                                  cout, kh, kw, strides[0], strides[1], pads[0], pads[1], dilations[0], dilations[1],
                                  1, oh, ow, _ptr(bias), int(act), _ptr(y), _DTYPE_CODE.get(y.dtype, 0), int(kernel),
                                  _stream(stream)))
+    return y
+
+
+def conv2d_f32(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, strides=(1, 1), pads=(0, 0),
+               dilations=(1, 1), group: int = 1, out_hw=None, act: int = ACT_NONE, stream=None) -> torch.Tensor:
+    """Plain fp32 NCHW Conv (begin pads; out_hw defaults to symmetric padding)."""
+    assert x.dtype == torch.float32 and w.dtype == torch.float32 and x.is_contiguous() and w.is_contiguous()
+    n, c, h, wd = x.shape
+    cout, _, kh, kw = w.shape
+    if out_hw is None:
+        out_hw = ((h + 2 * pads[0] - dilations[0] * (kh - 1) - 1) // strides[0] + 1,
+                  (wd + 2 * pads[1] - dilations[1] * (kw - 1) - 1) // strides[1] + 1)
+    y = torch.empty((n, cout, *out_hw), dtype=torch.float32, device=x.device)
+    _check(lib().lcml_fp8_conv2d_f32(_ptr(x), _ptr(w), _ptr(bias), _ptr(y), n, c, h, wd, cout, kh, kw, strides[0],
+                                     strides[1], pads[0], pads[1], dilations[0], dilations[1], group, out_hw[0],
+                                     out_hw[1], int(act), _stream(stream)))
     return y
 
 

@@ -331,6 +331,26 @@ int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t
     return hip_status(lcml::launch_gemv_valu_f32(M, N, K, a, lda, b_packed, e, (hipStream_t)stream), fn);
 }
 
+int lcml_fp8_conv2d_f32(const float *x, const float *w, const float *bias, float *y, int64_t n, int64_t c, int64_t h,
+                        int64_t wd, int64_t cout, int64_t kh, int64_t kw, int64_t stride_h, int64_t stride_w,
+                        int64_t pad_h, int64_t pad_w, int64_t dil_h, int64_t dil_w, int64_t group, int64_t oh,
+                        int64_t ow, int act, void *stream) {
+    const char *fn = "lcml_fp8_conv2d_f32";
+    if (n < 0 || c <= 0 || h <= 0 || wd <= 0 || cout <= 0 || kh <= 0 || kw <= 0 || oh <= 0 || ow <= 0 ||
+        group <= 0 || c % group != 0 || cout % group != 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: bad shape or group", fn);
+    if (stride_h <= 0 || stride_w <= 0 || dil_h <= 0 || dil_w <= 0 || pad_h < 0 || pad_w < 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: strides and dilations must be >= 1, pads >= 0", fn);
+    if (act < LCML_ACT_NONE || act > LCML_ACT_GELU_TANH) return fail(LCML_ERR_UNSUPPORTED, "%s: activation %d", fn, act);
+    if (n == 0) return LCML_OK;
+    if (!x || !w || !y) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (n * cout * oh * ow >= (int64_t)1 << 40) return fail(LCML_ERR_UNSUPPORTED, "%s: output too large", fn);
+    return hip_status(lcml::launch_conv2d_f32(x, w, bias, y, n, (int)c, (int)h, (int)wd, (int)cout, (int)kh, (int)kw,
+                                              (int)stride_h, (int)stride_w, (int)pad_h, (int)pad_w, (int)dil_h,
+                                              (int)dil_w, (int)group, (int)oh, (int)ow, act, (hipStream_t)stream),
+                      fn);
+}
+
 int lcml_fp8_sgemm(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, int trans_a, const float *b,
                    int64_t ldb, int trans_b, float alpha, const float *c, int c_ndim, int64_t c_dim0,
                    int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy, void *stream) {

@@ -60,7 +60,51 @@ __global__ __launch_bounds__(256) void k_activation(const float *__restrict__ x,
         y[i] = apply_act(x[i], act);
 }
 
+// Direct fp32 NCHW convolution, one thread per output element, one fma
+// chain per output in the reference Conv's reduction order (kh, kw, then the
+// group's input channels; conv.cpp:143-192, whose 4-wide partial sums differ
+// from this chain only in fp32 rounding), begin pads only (conv.cpp:121),
+// dilation, groups, bias, activation.
+__global__ __launch_bounds__(256) void k_conv2d_f32(const float *__restrict__ x, const float *__restrict__ w,
+                                                    const float *__restrict__ bias, float *__restrict__ y, int C,
+                                                    int H, int W, int Cout, int KH, int KW, int sh, int sw, int ph,
+                                                    int pw, int dh, int dw, int group, int OH, int OW, int act,
+                                                    int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int ow = (int)(i % OW);
+    const int oh = (int)((i / OW) % OH);
+    const int co = (int)((i / ((int64_t)OW * OH)) % Cout);
+    const int64_t n = i / ((int64_t)OW * OH * Cout);
+    const int cg = C / group, mg = Cout / group, g = co / mg;
+    const float *xn = x + (n * C + (int64_t)g * cg) * H * W;
+    const float *wc = w + (int64_t)co * cg * KH * KW;
+    float sum = 0.0f;
+    for (int kh = 0; kh < KH; ++kh) {
+        const int ih = oh * sh + kh * dh - ph;
+        if ((unsigned)ih >= (unsigned)H) continue;
+        for (int kw = 0; kw < KW; ++kw) {
+            const int iw = ow * sw + kw * dw - pw;
+            if ((unsigned)iw >= (unsigned)W) continue;
+            for (int c = 0; c < cg; ++c)
+                sum = fmaf(xn[((int64_t)c * H + ih) * W + iw], wc[((int64_t)c * KH + kh) * KW + kw], sum);
+        }
+    }
+    if (bias) sum += bias[co];
+    y[i] = apply_act(sum, act);
+}
+
 }  // namespace
+
+hipError_t launch_conv2d_f32(const float *x, const float *w, const float *bias, float *y, int64_t Nb, int C, int H,
+                             int W, int Cout, int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw,
+                             int group, int OH, int OW, int act, hipStream_t s) {
+    const int64_t total = Nb * Cout * OH * OW;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_conv2d_f32, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, w, bias, y, C, H, W,
+                       Cout, KH, KW, sh, sw, ph, pw, dh, dw, group, OH, OW, act, total);
+    return hipGetLastError();
+}
 
 hipError_t launch_sgemm(int64_t M, int64_t N, int64_t K, const float *A, int64_t lda, int transA, const float *B,
                         int64_t ldb, int transB, const Epilogue &e, hipStream_t s) {

@@ -56,6 +56,9 @@ hipError_t launch_gemv_valu_fp8(int64_t M, int64_t N, int64_t K, const uint8_t *
 
 hipError_t launch_sgemm(int64_t M, int64_t N, int64_t K, const float *A, int64_t lda, int transA, const float *B,
                         int64_t ldb, int transB, const Epilogue &e, hipStream_t s);
+hipError_t launch_conv2d_f32(const float *x, const float *w, const float *bias, float *y, int64_t Nb, int C, int H,
+                             int W, int Cout, int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw,
+                             int group, int OH, int OW, int act, hipStream_t s);
 hipError_t launch_activation(const float *x, float *y, int64_t n, int act, hipStream_t s);
 
 }  // namespace lcml

@@ -278,5 +278,9 @@ inline std::string attr_string(const Node &n, std::string_view name, std::string
     auto *a = n.try_get_attr(name);
     return a ? a->get<AttributeType::STRING>() : def;
 }
+inline std::vector<int32_t> attr_ints(const Node &n, std::string_view name, std::vector<int32_t> def) {
+    auto *a = n.try_get_attr(name);
+    return a ? a->get<AttributeType::INTS>() : def;
+}
 
 }  // namespace lcml::onnx

@@ -114,7 +114,9 @@ void NetworkInstance::create_tensor_for_var(const Variable &var) {
 // QDQ fusion:  [x -> QuantizeLinear(s) -> DequantizeLinear(s)] or
 // [x -> DynamicQuantizeLinear -> DequantizeLinear] or plain fp32 A, and
 // DequantizeLinear(W_e4m3 constant, s_w) as B, into Gemm/MatMul, optionally
-// followed by Relu/Gelu, become one FP8Linear node.
+// followed by Relu/Gelu, become one FP8Linear node; the same with a quantised
+// activation into Conv (4-D E4M3 weight, group 1, cin % 16 == 0) becomes one
+// FP8Conv node.
 // ------------------------------------------------------------------------
 namespace {
 
@@ -148,80 +150,54 @@ void NetworkInstance::fuse_qdq_linear() {
     };
     auto prod_idx = [&](const std::string &v) { return producer.at(v); };
 
-    std::vector<bool> removed(nodes.size(), false);
-    std::unordered_map<size_t, Node> replacement;
-    for (size_t i = 0; i < nodes.size(); ++i) {
-        const Node &n = nodes[i];
-        const bool gemm = n.get_op_type() == "Gemm", matmul = n.get_op_type() == "MatMul";
-        if (!gemm && !matmul) continue;
-        if (gemm && attr_int(n, "transA", 0) != 0) continue;
-        const Variable &A = n.get_inputs()[0].get();
-        const Variable &B = n.get_inputs()[1].get();
-        // ---- B = DequantizeLinear(W_e4m3 constant, s_w [, 0]) ----
-        const Node *dqw = prod(B.get_name());
-        if (!dqw || dqw->get_op_type() != "DequantizeLinear" || !only_consumer(B.get_name(), i)) continue;
-        const Variable &W = dqw->get_inputs()[0].get();
-        const Variable &sw = dqw->get_inputs()[1].get();
-        if (W.get_dtype() != DataType::FLOAT8E4M3FN || !W.is_constant() || W.get_shape().size() != 2) continue;
-        if (!sw.is_constant()) continue;
-        if (dqw->get_inputs().size() > 2 && !is_zero_constant(table_, dqw->get_inputs()[2].get())) continue;
-        const bool w_is_nk = gemm && attr_int(n, "transB", 0) != 0;
-        const size_t N = w_is_nk ? W.get_shape()[0] : W.get_shape()[1];
-        const size_t K = w_is_nk ? W.get_shape()[1] : W.get_shape()[0];
-        const size_t nscale = sw.num_elements();
-        if (nscale != 1) {
-            int axis = attr_int(*dqw, "axis", 1);
-            if (axis < 0) axis += 2;
-            const int n_axis = w_is_nk ? 0 : 1;
-            if (axis != n_axis || nscale != N) continue;  // only per-output-channel scales fuse
-        }
-        if (A.get_shape().empty() || A.get_shape().back() != K) continue;
-        // ---- A: static QDQ, dynamic QDQ, or fp32 ----
-        int a_mode = 0;  // 0: fp32 (W8A32), 1: static scale, 2: dynamic per-tensor
-        const Variable *a_src = &A, *a_scale = nullptr;
-        std::vector<size_t> drop = {prod_idx(B.get_name())};
+    // Activation side of node `who`'s input A: static QDQ (a_mode 1),
+    // dynamic QDQ (2) or neither (0, A itself); the Q and DQ nodes to drop.
+    struct ActQ {
+        int a_mode = 0;
+        const Variable *src = nullptr, *scale = nullptr;
+        std::vector<size_t> drop;
+    };
+    auto match_act = [&](const Variable &A, size_t who) {
+        ActQ r;
+        r.src = &A;
         const Node *dqa = prod(A.get_name());
-        if (dqa && dqa->get_op_type() == "DequantizeLinear" && only_consumer(A.get_name(), i)) {
-            const Variable &qv = dqa->get_inputs()[0].get();
-            const Node *q = prod(qv.get_name());
-            // the DQ zero point is a constant 0, or DynamicQuantizeLinear's own (zero) output
-            bool zp_ok = dqa->get_inputs().size() <= 2 || is_zero_constant(table_, dqa->get_inputs()[2].get()) ||
-                         (q && q->get_op_type() == "DynamicQuantizeLinear" && q->get_outputs().size() > 2 &&
-                          &q->get_outputs()[2].get() == &dqa->get_inputs()[2].get());
-            if (q && zp_ok && only_consumer(qv.get_name(), prod_idx(A.get_name())) &&
-                dqa->get_inputs()[1].get().num_elements() == 1) {
-                if (q->get_op_type() == "QuantizeLinear" &&
-                    &q->get_inputs()[1].get() == &dqa->get_inputs()[1].get() &&
-                    (q->get_inputs().size() <= 2 || is_zero_constant(table_, q->get_inputs()[2].get())) &&
-                    attr_int(*q, "saturate", 1) == 1) {
-                    a_mode = 1;
-                    a_src = &q->get_inputs()[0].get();
-                    a_scale = &q->get_inputs()[1].get();
-                } else if (q->get_op_type() == "DynamicQuantizeLinear" &&
-                           &q->get_outputs()[1].get() == &dqa->get_inputs()[1].get()) {
-                    bool private_outputs = true;
-                    for (size_t o = 0; o < q->get_outputs().size(); ++o) {
-                        const auto &on = q->get_outputs()[o].get().get_name();
-                        if (graph_outputs.count(on)) private_outputs = false;
-                        auto it = consumers.find(on);
-                        if (it != consumers.end())
-                            for (size_t c : it->second)
-                                if (c != prod_idx(A.get_name())) private_outputs = false;
-                    }
-                    if (private_outputs) {
-                        a_mode = 2;
-                        a_src = &q->get_inputs()[0].get();
-                    }
-                }
-                if (a_mode) {
-                    drop.push_back(prod_idx(A.get_name()));
-                    drop.push_back(prod_idx(qv.get_name()));
-                }
+        if (!dqa || dqa->get_op_type() != "DequantizeLinear" || !only_consumer(A.get_name(), who)) return r;
+        const Variable &qv = dqa->get_inputs()[0].get();
+        const Node *q = prod(qv.get_name());
+        // the DQ zero point is a constant 0, or DynamicQuantizeLinear's own (zero) output
+        bool zp_ok = dqa->get_inputs().size() <= 2 || is_zero_constant(table_, dqa->get_inputs()[2].get()) ||
+                     (q && q->get_op_type() == "DynamicQuantizeLinear" && q->get_outputs().size() > 2 &&
+                      &q->get_outputs()[2].get() == &dqa->get_inputs()[2].get());
+        if (!q || !zp_ok || !only_consumer(qv.get_name(), prod_idx(A.get_name())) ||
+            dqa->get_inputs()[1].get().num_elements() != 1)
+            return r;
+        if (q->get_op_type() == "QuantizeLinear" && &q->get_inputs()[1].get() == &dqa->get_inputs()[1].get() &&
+            (q->get_inputs().size() <= 2 || is_zero_constant(table_, q->get_inputs()[2].get())) &&
+            attr_int(*q, "saturate", 1) == 1) {
+            r.a_mode = 1;
+            r.src = &q->get_inputs()[0].get();
+            r.scale = &q->get_inputs()[1].get();
+        } else if (q->get_op_type() == "DynamicQuantizeLinear" &&
+                   &q->get_outputs()[1].get() == &dqa->get_inputs()[1].get()) {
+            bool private_outputs = true;
+            for (size_t o = 0; o < q->get_outputs().size(); ++o) {
+                const auto &on = q->get_outputs()[o].get().get_name();
+                if (graph_outputs.count(on)) private_outputs = false;
+                auto it = consumers.find(on);
+                if (it != consumers.end())
+                    for (size_t c : it->second)
+                        if (c != prod_idx(A.get_name())) private_outputs = false;
+            }
+            if (private_outputs) {
+                r.a_mode = 2;
+                r.src = &q->get_inputs()[0].get();
             }
         }
-        if (a_mode == 0 && A.get_dtype() != DataType::FLOAT) continue;
-        // ---- epilogue activation ----
-        const Variable *out = &n.get_outputs()[0].get();
+        if (r.a_mode) r.drop = {prod_idx(A.get_name()), prod_idx(qv.get_name())};
+        return r;
+    };
+    // a Relu/Gelu that is the only consumer of `out` becomes the epilogue
+    auto match_epilogue = [&](const Variable *&out, std::vector<size_t> &drop) {
         int act = LCML_ACT_NONE;
         auto cit = consumers.find(out->get_name());
         if (cit != consumers.end() && cit->second.size() == 1 && !graph_outputs.count(out->get_name())) {
@@ -234,6 +210,103 @@ void NetworkInstance::fuse_qdq_linear() {
                 out = &r.get_outputs()[0].get();
             }
         }
+        return act;
+    };
+    // B = DequantizeLinear(W_e4m3 constant of rank `rank`, constant scale [, 0]) feeding only `who`
+    auto match_weight = [&](const Variable &B, size_t who, size_t rank) -> const Node * {
+        const Node *dqw = prod(B.get_name());
+        if (!dqw || dqw->get_op_type() != "DequantizeLinear" || !only_consumer(B.get_name(), who)) return nullptr;
+        const Variable &W = dqw->get_inputs()[0].get();
+        if (W.get_dtype() != DataType::FLOAT8E4M3FN || !W.is_constant() || W.get_shape().size() != rank)
+            return nullptr;
+        if (!dqw->get_inputs()[1].get().is_constant()) return nullptr;
+        if (dqw->get_inputs().size() > 2 && !is_zero_constant(table_, dqw->get_inputs()[2].get())) return nullptr;
+        return dqw;
+    };
+
+    std::vector<bool> removed(nodes.size(), false);
+    std::unordered_map<size_t, Node> replacement;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        const Node &n = nodes[i];
+        if (n.get_op_type() == "Conv") {
+            // ---- DQ(x) , DQ(W_e4m3 [cout, cin, kh, kw]) -> Conv [-> act] ----
+            if (n.get_inputs().size() < 2 || attr_int(n, "group", 1) != 1 ||
+                attr_string(n, "auto_pad", "NOTSET") != "NOTSET")
+                continue;
+            const Variable &X = n.get_inputs()[0].get();
+            const Variable &Bv = n.get_inputs()[1].get();
+            const Node *dqw = match_weight(Bv, i, 4);
+            if (!dqw) continue;
+            const Variable &W = dqw->get_inputs()[0].get();
+            const Variable &sw = dqw->get_inputs()[1].get();
+            const auto &ws = W.get_shape();
+            const size_t cout = ws[0], cin = ws[1], kh = ws[2], kw = ws[3];
+            if (cin % 16 != 0) continue;
+            if (sw.num_elements() != 1 && !(sw.num_elements() == cout && attr_int(*dqw, "axis", 1) == 0)) continue;
+            if (X.get_shape().size() != 4 || X.get_shape()[1] != cin) continue;
+            ActQ aq = match_act(X, i);
+            if (aq.a_mode == 0) continue;  // FP8 conv needs a quantised activation
+            std::vector<size_t> drop = aq.drop;
+            drop.push_back(prod_idx(Bv.get_name()));
+            const Variable *out = &n.get_outputs()[0].get();
+            const int act = match_epilogue(out, drop);
+            std::string pname = W.get_name() + "::packed_conv";
+            if (!g.has_var(pname)) {
+                Variable pv(pname, DataType::FLOAT8E4M3FN, {kh * kw * cin, cout});
+                pv.set_is_constant(true);
+                g.add_variable(std::move(pv));
+            }
+            Node f(n.get_name().empty() ? "fp8_conv" : n.get_name() + "::fp8", "FP8Conv");
+            f.add_input(*aq.src);
+            f.add_input(g.get_var(pname));
+            f.add_input(sw);
+            if (aq.a_mode == 1) f.add_input(*aq.scale);
+            const bool has_bias = n.get_inputs().size() > 2;
+            if (has_bias) f.add_input(n.get_inputs()[2].get());
+            f.add_output(*out);
+            for (const char *a : {"strides", "pads", "dilations"})
+                if (auto *at = n.try_get_attr(a)) f.set_attribute(*at);
+            f.set_attribute(Attribute{"kernel_shape", std::vector<int32_t>{(int32_t)kh, (int32_t)kw}});
+            f.set_attribute(Attribute{"a_mode", (int32_t)aq.a_mode});
+            f.set_attribute(Attribute{"has_bias", (int32_t)has_bias});
+            f.set_attribute(Attribute{"act", (int32_t)act});
+            f.set_attribute(Attribute{"weight", W.get_name()});
+            for (size_t d : drop) removed[d] = true;
+            replacement.emplace(i, std::move(f));
+            ++fused_count_;
+            continue;
+        }
+        const bool gemm = n.get_op_type() == "Gemm", matmul = n.get_op_type() == "MatMul";
+        if (!gemm && !matmul) continue;
+        if (gemm && attr_int(n, "transA", 0) != 0) continue;
+        const Variable &A = n.get_inputs()[0].get();
+        const Variable &B = n.get_inputs()[1].get();
+        // ---- B = DequantizeLinear(W_e4m3 constant, s_w [, 0]) ----
+        const Node *dqw = match_weight(B, i, 2);
+        if (!dqw) continue;
+        const Variable &W = dqw->get_inputs()[0].get();
+        const Variable &sw = dqw->get_inputs()[1].get();
+        const bool w_is_nk = gemm && attr_int(n, "transB", 0) != 0;
+        const size_t N = w_is_nk ? W.get_shape()[0] : W.get_shape()[1];
+        const size_t K = w_is_nk ? W.get_shape()[1] : W.get_shape()[0];
+        const size_t nscale = sw.num_elements();
+        if (nscale != 1) {
+            int axis = attr_int(*dqw, "axis", 1);
+            if (axis < 0) axis += 2;
+            const int n_axis = w_is_nk ? 0 : 1;
+            if (axis != n_axis || nscale != N) continue;  // only per-output-channel scales fuse
+        }
+        if (A.get_shape().empty() || A.get_shape().back() != K) continue;
+        // ---- A: static QDQ, dynamic QDQ, or fp32 ----
+        ActQ aq = match_act(A, i);
+        const int a_mode = aq.a_mode;  // 0: fp32 (W8A32), 1: static scale, 2: dynamic per-tensor
+        const Variable *a_src = aq.src, *a_scale = aq.scale;
+        std::vector<size_t> drop = {prod_idx(B.get_name())};
+        drop.insert(drop.end(), aq.drop.begin(), aq.drop.end());
+        if (a_mode == 0 && A.get_dtype() != DataType::FLOAT) continue;
+        // ---- epilogue activation ----
+        const Variable *out = &n.get_outputs()[0].get();
+        const int act = match_epilogue(out, drop);
         // ---- build the fused node ----
         std::string pname = W.get_name() + "::packed";
         if (!g.has_var(pname)) {
@@ -274,7 +347,8 @@ void NetworkInstance::fuse_qdq_linear() {
 // at model load into MFMA-fragment order with their fp32 scales).
 void NetworkInstance::pack_weights() {
     for (const Node &n : model_.get_graph().get_nodes()) {
-        if (n.get_op_type() != "FP8Linear") continue;
+        const bool conv = n.get_op_type() == "FP8Conv";
+        if (n.get_op_type() != "FP8Linear" && !conv) continue;
         const Variable &pv = n.get_inputs()[1].get();
         if (table_.contains(pv.get_name())) continue;
         const Variable &W = model_.get_graph().get_var(attr_string(n, "weight", ""));
@@ -284,9 +358,14 @@ void NetworkInstance::pack_weights() {
         const uint32_t K = (uint32_t)pv.get_shape()[0], N = (uint32_t)pv.get_shape()[1];
         DeviceArray<uint8_t> packed((size_t)lcml_fp8_packed_weight_bytes(K, N));
         ITensor &wt = table_.at(W.get_name());
-        lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,
-                                        attr_int(n, "w_is_nk", 0), packed.data(), stream_),
-                   "pack weight");
+        if (conv)
+            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), wt.shape(0),
+                                                 wt.shape(1), wt.shape(2), wt.shape(3), packed.data(), stream_),
+                       "pack conv weight");
+        else
+            lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,
+                                            attr_int(n, "w_is_nk", 0), packed.data(), stream_),
+                       "pack weight");
         ITensor &st = table_.at(sw.get_name());
         DeviceArray<float> scale(static_cast<float *>(st.device_data()), 0, st.size());
         table_.own(pv.get_name(), std::make_unique<PackedWeightTensor>(K, N, std::move(packed), std::move(scale)));

@@ -9,7 +9,10 @@
 //   3. static activation QDQ -> Gemm(transB=1, per-channel weights) -> Gelu;
 //   4. DynamicQuantizeLinear -> DequantizeLinear -> MatMul(per-channel W);
 //   5. standalone QuantizeLinear / DequantizeLinear / Cast, bit-exact;
-//   6. error behaviour (dtype mismatch on bind, FP8 blob size rule).
+//   6. error behaviour (dtype mismatch on bind, FP8 blob size rule);
+//   7. DynamicQuantizeLinear -> DQ -> Conv(DQ(W), B) -> Relu, fused into
+//      FP8Conv and op by op, against the oracle's direct conv;
+//   8. an fp32 grouped / strided / dilated Conv.
 //   usage: test_network <tests/golden dir>
 #include <cmath>
 #include <cstdio>
@@ -33,6 +36,9 @@ float orc_amax(const float *, int64_t);
 float orc_scale_from_amax(float);
 void orc_gemm(int64_t, int64_t, int64_t, const float *, int, const float *, int, float, float, const float *, int,
               int64_t, int64_t, int, float *);
+void orc_conv2d(const float *, const float *, const float *, float *, int64_t, int64_t, int64_t, int64_t, int64_t,
+                int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                int);
 void orc_gemm_abs_bound(int64_t, int64_t, int64_t, const float *, int, const float *, int, float, float,
                         const float *, int, int64_t, int64_t, double *);
 }
@@ -367,6 +373,115 @@ static void test_dynamic_qdq_matmul() {
     }
 }
 
+// DynamicQuantizeLinear -> DequantizeLinear -> Conv(DQ(W_e4m3, per-channel
+// axis 0), B) -> Relu, fused into FP8Conv and op by op (fp32 Conv), both
+// against the oracle's direct conv of the dequantised operands; then an fp32
+// grouped Conv on its own.
+static void test_qdq_conv(bool fused) {
+    std::printf("[7] DynamicQuantizeLinear -> DQ -> Conv(DQ(W), B) -> Relu (%s)\n", fused ? "fused" : "op by op");
+    const int64_t Nb = 2, C = 32, H = 9, W = 11, CO = 24, KH = 3, KW = 3, OH = 9, OW = 11;
+    auto x = normals(71, (size_t)(Nb * C * H * W), 1.0f), w = normals(72, (size_t)(CO * C * KH * KW), 0.05f);
+    auto bias = normals(73, (size_t)CO, 0.01f);
+    const int64_t kper = C * KH * KW;
+    std::vector<float> sw(CO, 0.0f);
+    for (int64_t o = 0; o < CO; ++o)
+        for (int64_t k = 0; k < kper; ++k) sw[o] = std::max(sw[o], std::fabs(w[o * kper + k]));
+    for (auto &v : sw) v = orc_scale_from_amax(v);
+    std::vector<uint8_t> qw(w.size());
+    orc_quantize(w.data(), qw.data(), 1, CO, kper, sw.data());  // per output channel (axis 0)
+    Graph g("conv");
+    Blob blob;
+    var(g, "x", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    blob_var(g, blob, "W", DataType::FLOAT8E4M3FN, {(size_t)CO, (size_t)C, (size_t)KH, (size_t)KW}, qw.data(),
+             qw.size());
+    blob_var(g, blob, "sw", DataType::FLOAT, {(size_t)CO}, sw.data(), CO * 4);
+    blob_var(g, blob, "B", DataType::FLOAT, {(size_t)CO}, bias.data(), CO * 4);
+    var(g, "xq", DataType::FLOAT8E4M3FN, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    var(g, "xs", DataType::FLOAT, {1});
+    var(g, "xz", DataType::FLOAT8E4M3FN, {1});
+    var(g, "xd", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    var(g, "Wf", DataType::FLOAT, {(size_t)CO, (size_t)C, (size_t)KH, (size_t)KW});
+    var(g, "c", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
+    var(g, "y", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
+    node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
+    node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+    node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"}, {Attribute{"axis", (int32_t)0}});
+    node(g, "Conv", {"xd", "Wf", "B"}, {"c"},
+         {Attribute{"kernel_shape", std::vector<int32_t>{3, 3}}, Attribute{"pads", std::vector<int32_t>{1, 1, 1, 1}}});
+    node(g, "Relu", {"c"}, {"y"});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    DeviceBuffer wb(blob.bytes.size());
+    CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+    auto xt = upload(x, {(uint32_t)Nb, (uint32_t)C, (uint32_t)H, (uint32_t)W});
+    auto yt = make_device_tensor<float>({(uint32_t)Nb, (uint32_t)CO, (uint32_t)OH, (uint32_t)OW});
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_fusion(fused);
+    net.set_weight_buffer(wb.data(), blob.bytes.size());
+    net.set_input("x", *xt);
+    net.set_output("y", *yt);
+    net.forward();
+    auto y = download<float>(*yt);
+    if (fused) CHECK(net.fused_linear_count() == 1 && net.executed_op_types().size() == 1 &&
+                     net.executed_op_types()[0] == "FP8Conv");
+    else CHECK(net.executed_op_types().size() == 5);
+    float sx = orc_scale_from_amax(orc_amax(x.data(), x.size()));
+    std::vector<uint8_t> qx(x.size());
+    orc_quantize(x.data(), qx.data(), 1, 1, x.size(), &sx);
+    std::vector<float> A(x.size()), Bw(w.size()), ref(y.size()), absA(x.size()), absB(w.size()), bnd(y.size());
+    orc_dequantize(qx.data(), A.data(), 1, 1, qx.size(), &sx);
+    orc_dequantize(qw.data(), Bw.data(), 1, CO, kper, sw.data());
+    orc_conv2d(A.data(), Bw.data(), bias.data(), ref.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, 1, OH, OW,
+               LCML_ACT_RELU);
+    for (size_t i = 0; i < A.size(); ++i) absA[i] = std::fabs(A[i]);
+    for (size_t i = 0; i < Bw.size(); ++i) absB[i] = std::fabs(Bw[i]);
+    std::vector<float> absb(bias.size());
+    for (size_t i = 0; i < bias.size(); ++i) absb[i] = std::fabs(bias[i]);
+    orc_conv2d(absA.data(), absB.data(), absb.data(), bnd.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, 1, OH, OW,
+               LCML_ACT_NONE);
+    std::vector<double> bound(bnd.begin(), bnd.end());
+    CHECK(close(y, ref, bound, 1e-4, 0.0, fused ? "fused qdq conv" : "qdq conv op by op"));
+}
+
+static void test_f32_grouped_conv() {
+    std::printf("[8] fp32 Conv, group 2, stride 2, dilation 2\n");
+    const int64_t Nb = 1, C = 8, H = 12, W = 10, CO = 6, KH = 3, KW = 3, G = 2;
+    const int64_t OH = (H + 2 - 2 * (KH - 1) - 1) / 2 + 1, OW = (W + 2 - 2 * (KW - 1) - 1) / 2 + 1;
+    auto x = normals(81, (size_t)(Nb * C * H * W), 1.0f), w = normals(82, (size_t)(CO * (C / G) * KH * KW), 0.3f);
+    Graph g("conv32");
+    Blob blob;
+    var(g, "x", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    blob_var(g, blob, "W", DataType::FLOAT, {(size_t)CO, (size_t)(C / G), (size_t)KH, (size_t)KW}, w.data(), w.size() * 4);
+    var(g, "y", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
+    node(g, "Conv", {"x", "W"}, {"y"},
+         {Attribute{"group", (int32_t)G}, Attribute{"strides", std::vector<int32_t>{2, 2}},
+          Attribute{"dilations", std::vector<int32_t>{2, 2}}, Attribute{"pads", std::vector<int32_t>{1, 1, 1, 1}}});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    DeviceBuffer wb(blob.bytes.size());
+    CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+    auto xt = upload(x, {(uint32_t)Nb, (uint32_t)C, (uint32_t)H, (uint32_t)W});
+    auto yt = make_device_tensor<float>({(uint32_t)Nb, (uint32_t)CO, (uint32_t)OH, (uint32_t)OW});
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_weight_buffer(wb.data(), blob.bytes.size());
+    net.set_input("x", *xt);
+    net.set_output("y", *yt);
+    net.forward();
+    auto y = download<float>(*yt);
+    std::vector<float> ref(y.size());
+    orc_conv2d(x.data(), w.data(), nullptr, ref.data(), Nb, C, H, W, CO, KH, KW, 2, 2, 1, 1, 2, 2, G, OH, OW,
+               LCML_ACT_NONE);
+    std::vector<double> bound(y.size(), 0.0);
+    for (size_t i = 0; i < ref.size(); ++i) bound[i] = std::fabs(ref[i]) + 1.0;
+    CHECK(close(y, ref, bound, 1e-5, 0.0, "fp32 grouped conv"));
+}
+
 static void test_standalone_qdq_cast() {
     std::printf("[5] standalone QuantizeLinear / DequantizeLinear / Cast (bit-exact)\n");
     const int R = 8, C = 100;
@@ -471,6 +586,9 @@ int main(int argc, char **argv) {
         test_static_qdq_gelu();
         test_dynamic_qdq_matmul();
         test_standalone_qdq_cast();
+        test_qdq_conv(true);
+        test_qdq_conv(false);
+        test_f32_grouped_conv();
         test_errors();
     } catch (const Error &e) {
         std::printf("FAIL: uncaught error: %s\n", e.what());

@@ -128,3 +128,19 @@ def test_conv_errors(dev):
     bp = capi.pack_conv_weight(torch.zeros((4, 8, 3, 3), dtype=torch.uint8, device=dev))
     with pytest.raises(capi.LcmlError):
         capi.conv2d(xq, s, bp, s, 4, (3, 3), pads=(1, 1))
+
+
+@pytest.mark.parametrize("case", [(2, 6, 9, 11, 8, 3, 3, 1, 1, 1, 1), (1, 8, 12, 12, 12, 3, 3, 2, 1, 1, 2),
+                                  (1, 4, 10, 10, 6, 5, 5, 1, 2, 2, 1), (2, 16, 7, 7, 16, 1, 1, 1, 0, 1, 4)])
+@pytest.mark.parametrize("act", [capi.ACT_NONE, capi.ACT_RELU])
+def test_conv_f32_matches_oracle(dev, case, act):
+    """The plain fp32 Conv (groups, strides, dilation) against the oracle."""
+    n, c, h, w, cout, kh, kw, stride, pad, dil, group = case
+    x = synth.normal(c + h, (n, c, h, w))
+    wt = synth.normal(cout + kh, (cout, c // group, kh, kw), std=0.2)
+    b = synth.normal(3, (cout,), std=0.1)
+    st, pd, dl = (stride, stride), (pad, pad), (dil, dil)
+    y = capi.conv2d_f32(to_dev(x, dev), to_dev(wt, dev), to_dev(b, dev), st, pd, dl, group, act=act)
+    ref = oracle.conv2d(x, wt, b, strides=st, pads=pd, dilations=dl, group=group, act=act)
+    bound = oracle.conv2d(np.abs(x), np.abs(wt), np.abs(b), strides=st, pads=pd, dilations=dl, group=group)
+    assert_close(y.cpu().numpy(), ref, bound, act=act)
