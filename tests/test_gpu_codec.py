@@ -59,6 +59,30 @@ def test_quantize_exhaustive_all_fp32_patterns(dev):
         del x
 
 
+@pytest.mark.parametrize("scale", [0.0137, 1.0 / 448.0])
+def test_quantize_exhaustive_all_fp32_patterns_scaled(dev, scale):
+    """Every fp32 bit pattern through lcml_fp8_quantize with a non-trivial
+    per-tensor scale: the kernel's reciprocal division + hardware conversion
+    against the oracle's IEEE x / s + encoder."""
+    chunk = 1 << 28
+    sd = torch.tensor([scale], dtype=torch.float32, device=dev)
+    y = torch.empty(chunk, dtype=torch.uint8, device=dev)
+    s32 = np.float32(scale)
+    base = np.arange(chunk, dtype=np.uint32)
+    bits = np.empty(chunk, dtype=np.uint32)
+    for c in range((1 << 32) // chunk):
+        first = c * chunk
+        x = _int32_bits(first, chunk, dev).view(torch.float32)
+        capi.quantize(x, sd, out=y)
+        got = y.cpu().numpy()
+        np.add(base, np.uint32(first), out=bits)
+        ref = oracle.quantize(bits.view(np.float32), s32)
+        if not np.array_equal(got, ref):
+            i = int(np.flatnonzero(got != ref)[0])
+            pytest.fail(f"scale {scale}: pattern 0x{first + i:08x}: gpu 0x{got[i]:02x} oracle 0x{ref[i]:02x}")
+        del x
+
+
 @pytest.mark.parametrize("n", [0, 1, 15, 16, 17, 1000, 4096, 65537, 1 << 20])
 @pytest.mark.parametrize("offset", [0, 1])
 def test_quantize_per_tensor(dev, n, offset):
