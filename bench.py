@@ -183,21 +183,30 @@ def main() -> int:
     if os.path.exists(tpath):
         with open(tpath) as fh:
             tj = json.load(fh)
-        if tj.get("kernel_key") == "skinny_dynamic":  # counters of the kernel this line reports
+        if tj.get("kernel_key") == "skinny_step":  # counters of the kernel launches this line reports
             traffic_bytes = tj["mean_hbm_bytes"]
-            traffic_src = ("profiles/skinny_gemm_small_m_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                           "copy-calibrated, mean over M)")
+            traffic_src = ("profiles/skinny_gemm_small_m_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per "
+                           "dispatch, copy-calibrated, mean over M)")
     value_gbs = bytes_step / (step_ms * 1e-3) / 1e9
     kbytes = sum(gemm_kernel_bytes(M) for M in SMALL_MS)
     k_gbs = kbytes / (gemm_ms_total * 1e-3) / 1e9
-    # the fused kernel is the whole linear: its per-M average launch duration
-    per_launch = {}
+    # The dominant kernel is k_gemm_skinny: the fused-quantise instantiation
+    # is the whole linear where AUTO fuses (fp32 activations in), the E4M3
+    # instantiation after the quantise kernel elsewhere.  Per M, the average
+    # duration of that kernel's launches (a graph holding only them).
+    per_launch, kern_bytes, fused_m = {}, {}, {}
     for M in SMALL_MS:
-        gm = capture(lambda i, M=M: linear(M, i % N_WEIGHT_COPIES), 3 * args.steps)
+        fused_m[M] = capi.lib().lcml_fp8_gemm_dynamic_workspace_bytes(M, K, capi.KERNEL_AUTO) == 0
+        if fused_m[M]:
+            fn, kern_bytes[str(M)] = (lambda i, M=M: linear(M, i % N_WEIGHT_COPIES)), small_m_bytes(M)
+        else:
+            fn, kern_bytes[str(M)] = ((lambda i, M=M: linear_two_kernel(M, i % N_WEIGHT_COPIES, gemm_only=True)),
+                                      gemm_kernel_bytes(M))
+        gm = capture(fn, 3 * args.steps)
         gm.replay()
         per_launch[str(M)] = round(1e3 * timed(gm.replay) / (3 * args.steps), 2)
         del gm
-    fused_gbs = bytes_step / (sum(per_launch.values()) * 1e-6) / 1e9
+    kern_gbs = sum(kern_bytes.values()) / (sum(per_launch.values()) * 1e-6) / 1e9
     out.update({
         "value": round(value_gbs, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 5),
         "ms_per_step_eager_launches": round(eager_ms, 5),
@@ -208,12 +217,14 @@ def main() -> int:
                    "K": K, "N": N, "M": list(SMALL_MS), "weight_copies_rotated": N_WEIGHT_COPIES,
                    "bytes_per_step": bytes_step, "pct_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_gemm_skinny, exact bf16-MFMA instantiation, with fused dynamic quantisation "
-                               "where AUTO fuses (per-M launch = the whole linear)",
-                     "achieved": round(fused_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
+                     "kernel": "k_gemm_skinny, exact bf16-MFMA instantiation (fused dynamic quantisation at "
+                               + ",".join(f"M={M}" for M in SMALL_MS if fused_m[M]) + ", E4M3 activations in "
+                               "at " + ",".join(f"M={M}" for M in SMALL_MS if not fused_m[M]) + ")",
+                     "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
                      "traffic_source": traffic_src,
-                     "bytes_per_launch": {str(M): small_m_bytes(M) for M in SMALL_MS},
+                     "bytes_per_launch": kern_bytes,
+                     "bytes_per_launch_mean": round(sum(kern_bytes.values()) / len(kern_bytes)),
                      "avg_launch_us": per_launch},
         "two_kernel_composition": {
             "ms_per_step": round(two_ms, 5), "gbs": round(bytes_step / (two_ms * 1e-3) / 1e9, 1),

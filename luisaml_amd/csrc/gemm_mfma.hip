@@ -51,7 +51,12 @@ namespace {
 #define LCML_GEMM_WAVES_N 4
 #endif
 
-constexpr int BK = 128;
+#ifndef LCML_GEMM_STAGES
+#define LCML_GEMM_STAGES 4
+#endif
+constexpr int BK = 64;                    // K per pipeline step
+constexpr int NSTAGE = LCML_GEMM_STAGES;  // LDS ring depth: NSTAGE-1 steps of loads in flight
+constexpr int CPR = BK / 16;              // 16-byte chunks per A row per step
 constexpr int GROUP_M = 8;
 constexpr int EP_PITCH = 33;  // epilogue staging row pitch (floats)
 
@@ -67,10 +72,14 @@ struct Tile {
     static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
     static constexpr int BM = WAVES_M * WM * 32, BN = WAVES_N * WN * 32;
     static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
-    static constexpr int A_BLK = BM / 8 / NW, B_BLK = BN / 8 / NW;  // 1 KB load blocks per wavefront
+    static constexpr int A_BLK = A_BYTES / 1024 / NW, B_BLK = B_BYTES / 1024 / NW;  // 1 KB load blocks per wavefront
+    static constexpr int LOADS = A_BLK + B_BLK;  // load instructions per wavefront per step
     static constexpr int EP_BYTES = NW * WM * 32 * EP_PITCH * 4;
-    static constexpr int LDS_BYTES = 2 * STAGE > EP_BYTES ? 2 * STAGE : EP_BYTES;
-    static_assert(BM % 64 == 0 && BN % 64 == 0 && (BM / 8) % NW == 0 && (BN / 8) % NW == 0, "tile shape");
+    static constexpr int LDS_BYTES = NSTAGE * STAGE > EP_BYTES ? NSTAGE * STAGE : EP_BYTES;
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && (A_BYTES / 1024) % NW == 0 && (B_BYTES / 1024) % NW == 0,
+                  "tile shape");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(NSTAGE >= 3 && (NSTAGE - 2) * LOADS <= 63, "pipeline depth");
 };
 
 // Implicit-im2col convolution geometry (CONV instantiation).  A is the
@@ -109,7 +118,11 @@ __device__ inline v8i join(u4 lo, u4 hi) {
     return r;
 }
 
-__device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
+// A rows in LDS: chunk c of row r at chunk position c ^ swz(r); the 16 rows
+// of a ds_read_b128 lane group then cover all 16 16-byte bank slots of the
+// 64-bank LDS (BK=128: 2 rows per 256 B; BK=64: 4 rows per 256 B).
+__device__ inline int a_swz(int r) { return (r / (256 / BK)) & (CPR - 1); }
+__device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) << 4); }
 
 template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV>
 __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs g) {
@@ -131,7 +144,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
     const int64_t m0 = (int64_t)tm * T::BM, n0 = (int64_t)tn * T::BN;
 
     // ---- global -> LDS block assignment ----------------------------------
-    // A: 1 KB block b holds rows 8b..8b+7; B: block b holds panel b/8, k-chunk b%8.
+    // A: 1 KB block b holds rows (1024/BK)*b ..; B: block b holds panel b/CPR,
+    // k-chunk b%CPR of the step.
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, (int)g.a_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t b_rsrc =
@@ -142,8 +156,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
     int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
 #pragma unroll
     for (int i = 0; i < T::A_BLK; ++i) {
-        const int r = (wave * T::A_BLK + i) * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = (wave * T::A_BLK + i) * (1024 / BK) + lane / CPR;
+        const int c = (lane % CPR) ^ a_swz(r);
         a_kc[i] = c * 16;
         if constexpr (CONV) {
             // a_off = the row's image base n*H*W*C; rows past M get an input
@@ -163,8 +177,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
 #pragma unroll
     for (int i = 0; i < T::B_BLK; ++i) {
         const int b = wave * T::B_BLK + i;
-        const int64_t panel = (n0 >> 6) + (b >> 3);
-        b_off[i] = panel < g.npanels ? (uint32_t)((panel * g.KC + (b & 7)) * 1024 + lane * 16) : OOB;
+        const int64_t panel = (n0 >> 6) + b / CPR;
+        b_off[i] = panel < g.npanels ? (uint32_t)((panel * g.KC + b % CPR) * 1024 + lane * 16) : OOB;
     }
     auto issue_tile = [&](int kt, int stage) {
         uint8_t *sa = smem + stage * T::STAGE;
@@ -190,7 +204,9 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
         }
 #pragma unroll
         for (int i = 0; i < T::B_BLK; ++i) {
-            const uint32_t off = b_off[i] != OOB ? b_off[i] + (uint32_t)kt * 8 * 1024 : OOB;
+            // steps past the end (the pipeline tail) load whatever lies there
+            // into a stage that is never read again
+            const uint32_t off = b_off[i] != OOB ? b_off[i] + (uint32_t)kt * CPR * 1024 : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 b_rsrc, (lds_void *)(sa + T::A_BYTES + (wave * T::B_BLK + i) * 1024), 16, off, 0, 0, 0);
         }
@@ -210,61 +226,117 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
         const int col = wn * WN * 32 + j * 32;  // first column of this 32-column block in the tile
-        b_off_lds[j] = (col >> 6) * 8192 + ((col & 63) + (lane & 31)) * 16;
+        b_off_lds[j] = (col >> 6) * (CPR * 1024) + ((col & 63) + (lane & 31)) * 16;
     }
 
-    issue_tile(0, 0);
-    __syncthreads();
+    // Ring of NSTAGE LDS stages of one 64-k step each; every step issues
+    // exactly LOADS loads per wavefront (past-the-end steps load zeros or
+    // unused bytes into stages nobody reads).  The sync of step kt waits
+    // until tile kt+1 has landed (at most (NSTAGE-3)*LOADS loads of this
+    // wavefront outstanding), drains this wavefront's LDS reads (lgkmcnt(0),
+    // a wait the compiler sees), and barriers: after it every wavefront's
+    // share of tile kt+1 is visible and tile kt-1 is consumed everywhere, so
+    // its stage takes the prefetch of tile kt+NSTAGE-1.  The vmcnt wait is
+    // written out because the compiler's own accounting would wait for every
+    // load; sched_barrier(0) keeps LDS reads and MFMAs on their side of it.
+    auto step_sync = [&](auto outstanding) {
+        __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(decltype(outstanding)::value) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using Steady = std::integral_constant<int, (NSTAGE - 3) * T::LOADS>;
+    using First = std::integral_constant<int, (NSTAGE - 2) * T::LOADS>;
+    const uint8_t *stage0 = smem;
+    auto stage_a = [&](int kt) { return stage0 + (kt % NSTAGE) * T::STAGE; };
+    // one 16-byte k-chunk (chunk index c of the step) of every A and B block
+    auto read_chunk = [&](u4 (&fa)[WM], u4 (&fb)[WN], int kt, int c) {
+        const uint8_t *sa = stage_a(kt), *sb = sa + T::A_BYTES;
+#pragma unroll
+        for (int j = 0; j < WN; ++j) fb[j] = *reinterpret_cast<const u4 *>(sb + b_off_lds[j] + c * 1024);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) fa[i] = *reinterpret_cast<const u4 *>(sa + a_lds_off(a_r0 + i * 32, c));
+    };
 
-    for (int kt = 0; kt < g.nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < g.nk) issue_tile(kt + 1, cur ^ 1);
-        const uint8_t *sa = smem + cur * T::STAGE;
-        const uint8_t *sb = sa + T::A_BYTES;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int c0 = s * 4 + kgrp;
-            v8i bf[WN], af[WM];
+    for (int p = 0; p < NSTAGE - 1; ++p) issue_tile(p, p);
+    step_sync(First{});  // tile 0
+
+    if constexpr (EXACT) {
+        // Each lane's 64-k fragment is two 16-byte chunks (lo: chunk kgrp,
+        // hi: kgrp+1), each feeding two 32x32x16 bf16 MFMA groups (8 bytes
+        // per group, widened exactly).  The chunk of the next half is read
+        // while the MFMAs of the current half run: lo(kt) is read during the
+        // hi half of step kt-1, hi(kt) during the lo half of step kt.
+        u4 lo_a[WM], lo_b[WN], hi_a[WM], hi_b[WN];
+        auto mma_half = [&](const u4 (&fa)[WM], const u4 (&fb)[WN]) {
 #pragma unroll
-            for (int j = 0; j < WN; ++j) {
-                const uint8_t *p = sb + b_off_lds[j] + c0 * 1024;
-                bf[j] = join(*reinterpret_cast<const u4 *>(p), *reinterpret_cast<const u4 *>(p + 1024));
-            }
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 a16[WM], b16[WN];
 #pragma unroll
-            for (int i = 0; i < WM; ++i) {
-                const int r = a_r0 + i * 32;
-                af[i] = join(*reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0)),
-                             *reinterpret_cast<const u4 *>(sa + a_lds_off(r, c0 + 1)));
-            }
-            if constexpr (EXACT) {
-                // 64 k of each lane's fragment = 4 groups of 8; group q feeds the
-                // q-th 32x32x16 bf16 MFMA for both operands (the same k
-                // permutation on A and B, so the dot product is unchanged).  The
-                // WM*WN MFMAs of one group are independent of each other.
+                for (int i = 0; i < WM; ++i) a16[i] = h ? e4m3x8_to_bf16(fa[i].z, fa[i].w) : e4m3x8_to_bf16(fa[i].x, fa[i].y);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    bf16x8 a16[WM], b16[WN];
-#pragma unroll
-                    for (int i = 0; i < WM; ++i) a16[i] = e4m3x8_to_bf16((uint32_t)af[i][2 * q], (uint32_t)af[i][2 * q + 1]);
-#pragma unroll
-                    for (int j = 0; j < WN; ++j) b16[j] = e4m3x8_to_bf16((uint32_t)bf[j][2 * q], (uint32_t)bf[j][2 * q + 1]);
-#pragma unroll
-                    for (int i = 0; i < WM; ++i)
-#pragma unroll
-                        for (int j = 0; j < WN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
-                }
-            } else {
+                for (int j = 0; j < WN; ++j) b16[j] = h ? e4m3x8_to_bf16(fb[j].z, fb[j].w) : e4m3x8_to_bf16(fb[j].x, fb[j].y);
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
 #pragma unroll
                     for (int j = 0; j < WN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0,
-                                                                                    0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
             }
+        };
+        read_chunk(lo_a, lo_b, 0, kgrp);
+        for (int kt = 0; kt < g.nk; ++kt) {
+            read_chunk(hi_a, hi_b, kt, kgrp + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma_half(lo_a, lo_b);
+            step_sync(Steady{});  // tile kt+1
+            issue_tile(kt + NSTAGE - 1, (kt + NSTAGE - 1) % NSTAGE);
+            read_chunk(lo_a, lo_b, kt + 1, kgrp);  // past the end: an unused stage
+            __builtin_amdgcn_sched_barrier(0);
+            mma_half(hi_a, hi_b);
         }
-        __syncthreads();
+    } else {
+        // 32x32x64 FP8 MFMAs take the whole 32-byte fragment; the fragments
+        // of step kt+1 are read (second register set) while step kt's run.
+        // nk is even (K is padded to 128), so steps come in pairs.
+        u4 a0[WM][2], b0[WN][2], a1[WM][2], b1[WN][2];
+        auto read_frag = [&](u4 (&fa)[WM][2], u4 (&fb)[WN][2], int kt) {
+            u4 ta[WM], tb[WN];
+            read_chunk(ta, tb, kt, kgrp);
+#pragma unroll
+            for (int i = 0; i < WM; ++i) fa[i][0] = ta[i];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) fb[j][0] = tb[j];
+            read_chunk(ta, tb, kt, kgrp + 1);
+#pragma unroll
+            for (int i = 0; i < WM; ++i) fa[i][1] = ta[i];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) fb[j][1] = tb[j];
+        };
+        auto mma = [&](const u4 (&fa)[WM][2], const u4 (&fb)[WN][2]) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(join(fa[i][0], fa[i][1]),
+                                                                                join(fb[j][0], fb[j][1]), acc[i][j], 0,
+                                                                                0, 0, 0, 0, 0);
+        };
+        read_frag(a0, b0, 0);
+        for (int kt = 0; kt < g.nk; kt += 2) {
+            step_sync(Steady{});  // tile kt+1
+            issue_tile(kt + NSTAGE - 1, (kt + NSTAGE - 1) % NSTAGE);
+            read_frag(a1, b1, kt + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(a0, b0);
+            step_sync(Steady{});  // tile kt+2
+            issue_tile(kt + NSTAGE, (kt + NSTAGE) % NSTAGE);
+            read_frag(a0, b0, kt + 2);  // past the end: an unused stage
+            __builtin_amdgcn_sched_barrier(0);
+            mma(a1, b1);
+        }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tail's loads land before the LDS is reused
+    __syncthreads();
 
     // ---- epilogue --------------------------------------------------------
     // The accumulators go through LDS (free after the last barrier) one
