@@ -54,6 +54,9 @@ namespace {
 #ifndef LCML_GEMM_STAGES
 #define LCML_GEMM_STAGES 4
 #endif
+#ifndef LCML_GEMM_WG_PER_CU
+#define LCML_GEMM_WG_PER_CU 1  // occupancy the register budget is sized for
+#endif
 constexpr int BK = 64;                    // K per pipeline step
 constexpr int NSTAGE = LCML_GEMM_STAGES;  // LDS ring depth: NSTAGE-1 steps of loads in flight
 constexpr int CPR = BK / 16;              // 16-byte chunks per A row per step
@@ -125,7 +128,7 @@ __device__ inline int a_swz(int r) { return (r / (256 / BK)) & (CPR - 1); }
 __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) << 4); }
 
 template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV>
-__global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs g) {
+__global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_gemm_mfma(GemmArgs g) {
     using T = Tile<WAVES_M, WAVES_N, WM, WN>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -154,6 +157,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
     int a_kc[T::A_BLK];
     uint32_t b_off[T::B_BLK];
     int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
+    // CONV: where the block's chunk of the next step to issue lies in (kh, kw, c)
+    int a_c[CONV ? T::A_BLK : 1], a_kw[CONV ? T::A_BLK : 1], a_kh[CONV ? T::A_BLK : 1];
 #pragma unroll
     for (int i = 0; i < T::A_BLK; ++i) {
         const int r = (wave * T::A_BLK + i) * (1024 / BK) + lane / CPR;
@@ -170,6 +175,14 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
             a_off[i] = n * (uint32_t)(cv.H * cv.W * cv.C);
             a_ih0[i] = m < g.M ? (int)oh * cv.sh - cv.ph : -(1 << 30);
             a_iw0[i] = (int)ow * cv.sw - cv.pw;
+            // step 0 starts at k = c*16 < 64 <= ... ; c*16 may still exceed C
+            // (C >= 16), so normalise once
+            int cc = c * 16, kw = 0, kh = 0;
+            while (cc >= cv.C) {
+                cc -= cv.C;
+                if (++kw == cv.KW) { kw = 0; ++kh; }
+            }
+            a_c[i] = cc; a_kw[i] = kw; a_kh[i] = kh;
         } else {
             a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
         }
@@ -187,15 +200,20 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
         for (int i = 0; i < T::A_BLK; ++i) {
             uint32_t off;
             if constexpr (CONV) {
-                // k -> (tap, channel) -> (kh, kw); C % 16 == 0 keeps every
-                // 16-byte chunk inside one tap
+                // k = kbyte + chunk -> (kh, kw, c), tracked incrementally:
+                // steps are issued in order, each advancing k by BK; C % 16
+                // == 0 keeps every 16-byte chunk inside one tap
                 const ConvGeom &cv = g.cv;
                 const uint32_t k = kbyte + (uint32_t)a_kc[i];
-                const uint32_t tap = k / (uint32_t)cv.C, cin = k - tap * (uint32_t)cv.C;
-                const uint32_t kh = tap / (uint32_t)cv.KW, kw = tap - kh * (uint32_t)cv.KW;
-                const int ih = a_ih0[i] + (int)kh * cv.dh, iw = a_iw0[i] + (int)kw * cv.dw;
+                const int ih = a_ih0[i] + a_kh[i] * cv.dh, iw = a_iw0[i] + a_kw[i] * cv.dw;
                 const bool ok = (int64_t)k < g.K && (uint32_t)ih < (uint32_t)cv.H && (uint32_t)iw < (uint32_t)cv.W;
-                off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.C + cin : OOB;
+                off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.C + (uint32_t)a_c[i]
+                         : OOB;
+                a_c[i] += BK;
+                while (a_c[i] >= cv.C) {
+                    a_c[i] -= cv.C;
+                    if (++a_kw[i] == cv.KW) { a_kw[i] = 0; ++a_kh[i]; }
+                }
             } else {
                 off = (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
             }
@@ -397,7 +415,13 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, 1) void k_gemm_mfma(GemmArgs
 }
 
 constexpr int WAVES_M = LCML_GEMM_WAVES_M, WAVES_N = LCML_GEMM_WAVES_N;
-constexpr int WM = 256 / 32 / WAVES_M, WN = 256 / 32 / WAVES_N;
+#ifndef LCML_GEMM_WM
+#define LCML_GEMM_WM 4
+#endif
+#ifndef LCML_GEMM_WN
+#define LCML_GEMM_WN 2
+#endif
+constexpr int WM = LCML_GEMM_WM, WN = LCML_GEMM_WN;  // 32x32 blocks per wavefront
 static_assert(WM % 2 == 0, "the NCHW epilogue walks 64-row halves");
 using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
 

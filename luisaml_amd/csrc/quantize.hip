@@ -178,10 +178,11 @@ __global__ void k_amax_to_float(const uint32_t *amax_bits, float *out) {
 }
 
 // Dynamic quantisation of a small tensor in ONE launch with no workspace:
-// each of the P workgroups reduces the amax of the whole tensor (float4
-// loads, L2-resident after the first workgroup touches it), then encodes
-// only its own 1/P slice, so the IEEE divide + encode work (~30 VALU ops per
-// element) is spread over P CUs instead of one.
+// each of the P = ceil(n/4096) workgroups loads the whole tensor (float4
+// loads, L2-resident after the first workgroup touches it) and reduces its
+// amax, then encodes only its own 4096-element slice from the registers it
+// already holds, so the encode work is spread over P CUs and x is read once
+// per workgroup.
 constexpr int kSmallThreads = 1024;
 constexpr int64_t kSmallMax = 65536;
 constexpr int kRedThreads = 1024;
@@ -191,26 +192,31 @@ __global__ __launch_bounds__(kRedThreads) void k_quantize_dynamic_spread(
     __shared__ float red[kRedThreads / 64];
     const f4 *x4 = reinterpret_cast<const f4 *>(x);
     float m = 0.0f;
-    constexpr int U = 16;  // 1024 threads x 16 float4 = the whole 64K-element tensor in one round trip
-    for (int64_t i0 = threadIdx.x; i0 < n4; i0 += (int64_t)kRedThreads * U) {
-        f4 v[U];
+    // 1024 threads x 16 float4 = the whole (at most 64K-element) tensor in
+    // one round trip; thread t holds float4 t + 1024*u in v[u]
+    constexpr int U = 16;
+    f4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t i = i0 + (int64_t)u * kRedThreads;
-            v[u] = i < n4 ? x4[i] : f4{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int u = 0; u < U; ++u) {
+        const int64_t i = threadIdx.x + (int64_t)u * kRedThreads;
+        v[u] = i < n4 ? x4[i] : f4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            m = absmax_acc(m, v[u].x); m = absmax_acc(m, v[u].y);
-            m = absmax_acc(m, v[u].z); m = absmax_acc(m, v[u].w);
-        }
+    for (int u = 0; u < U; ++u) {
+        m = absmax_acc(m, v[u].x); m = absmax_acc(m, v[u].y);
+        m = absmax_acc(m, v[u].z); m = absmax_acc(m, v[u].w);
     }
     m = block_max<kRedThreads>(m, red);
     const float s = scale_from_amax_bits(f32_bits(m));
     const Recip d = make_recip(s);
-    uint32_t *y4 = reinterpret_cast<uint32_t *>(y);
-    for (int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kRedThreads)
-        y4[i] = enc4(x4[i], d);
+    // workgroup b encodes float4s b*1024 + t, which thread t already holds
+    // in v[b]: no second read of x
+    f4 mine = v[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u)
+        if ((int)blockIdx.x == u) mine = v[u];
+    const int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x;
+    if (i < n4) reinterpret_cast<uint32_t *>(y)[i] = enc4(mine, d);
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s;
 }
 
@@ -293,10 +299,10 @@ hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float 
                                    uint32_t *work, hipStream_t s) {
     if (n <= kSmallMax) {
         if (n % 4 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(y) & 3) == 0) {
-            // one float4 per thread in the encode pass, at most 64 workgroups
+            // one float4 per thread in the encode pass: ceil(n4 / 1024) <= 16 workgroups
             const int64_t n4 = n / 4;
             int p = (int)((n4 + kRedThreads - 1) / kRedThreads);
-            p = p < 1 ? 1 : (p > 64 ? 64 : p);
+            p = p < 1 ? 1 : p;
             hipLaunchKernelGGL(k_quantize_dynamic_spread, dim3(p), dim3(kRedThreads), 0, s, x, y, n4, scale_out);
         } else
             hipLaunchKernelGGL(k_quantize_dynamic_small, dim3(1), dim3(kSmallThreads), 0, s, x, y, n,
