@@ -202,15 +202,20 @@ LCML_API int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64
                            const float *y_scale, float *scale_out, void *workspace, void *stream);
 
 /*
- * Conv weights: E4M3 [cout][cin][kh][kw] (ONNX Conv W layout, dense) packed
- * for lcml_fp8_conv2d: the GEMM weight with reduction index
- * k = (kh*KW + kw)*cin + c (the reference Conv's loop order kh, kw, then
- * channels, src/onnx/operators/conv.cpp:143-192) and columns = cout, in the
- * lcml_fp8_pack_weight panel layout.  Size:
- * lcml_fp8_packed_weight_bytes(kh*kw*cin, cout).
+ * Conv weights: E4M3 [cout][cin/group][kh][kw] (ONNX Conv W layout, dense)
+ * packed for lcml_fp8_conv2d.  For each group g (output channels
+ * g*cout/group ..), the GEMM weight with reduction index
+ * k = (kh*KW + kw)*cin_g + c (the reference Conv's loop order kh, kw, then
+ * channels, src/onnx/operators/conv.cpp:143-192) and cout/group columns, in
+ * the lcml_fp8_pack_weight panel layout; the groups' blocks follow one
+ * another.  Size: lcml_fp8_packed_conv_weight_bytes(...) =
+ * group * lcml_fp8_packed_weight_bytes(kh*kw*cin_g, cout/group).
+ * cin_g = input channels per group.
  */
-LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin, int64_t kh, int64_t kw,
-                              uint8_t *packed, void *stream);
+LCML_API int64_t lcml_fp8_packed_conv_weight_bytes(int64_t cout, int64_t cin_g, int64_t kh, int64_t kw,
+                                          int64_t group);
+LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin_g, int64_t kh, int64_t kw,
+                              int64_t group, uint8_t *packed, void *stream);
 
 /*
  * 2-D convolution with E4M3 input and weights, fp32 accumulation, as an
@@ -221,12 +226,14 @@ LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t c
  * with out-of-range input positions contributing zero.  pad_h/pad_w are the
  * BEGIN pads (the reference applies only those, conv.cpp:121; end pads only
  * enter through the output size oh x ow, which the caller passes).
- * x_nhwc: lcml_fp8_quantize_nhwc output; c % 16 == 0; group must be 1.
+ * x_nhwc: lcml_fp8_quantize_nhwc output; group divides c and cout, and
+ * (c/group) % 16 == 0 (group g reads channels g*c/group .. and writes output
+ * channels g*cout/group .., conv.cpp:139,158).
  * w_packed: lcml_fp8_pack_conv_weight output.  bias: cout floats or NULL.
  * y: NCHW [n][cout][oh][ow], y_dtype LCML_DTYPE_FLOAT or BFLOAT16.
  * kernel: LCML_KERNEL_AUTO / MFMA (exact bf16 matrix cores) or MFMA_FP8.
  * Replaces Conv::apply (src/onnx/operators/conv.cpp:115-207) for the
- * DQ(x), DQ(W) -> Conv [-> Relu] pattern.
+ * DQ(x), DQ(W) -> Conv [-> Relu/Gelu] pattern.
  */
 LCML_API int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int64_t c, int64_t h,
                     int64_t w, const uint8_t *w_packed, const float *w_scale, int w_scale_per_channel,

@@ -50,7 +50,8 @@ _SIGS = {
     "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
                                      _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
     "lcml_fp8_quantize_nhwc": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
-    "lcml_fp8_pack_conv_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "lcml_fp8_packed_conv_weight_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "lcml_fp8_pack_conv_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "lcml_fp8_conv2d": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int, _vp, _int, _int, _vp]),
     "lcml_fp8_conv2d_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -264,19 +265,21 @@ def quantize_nhwc(x: torch.Tensor, scale: torch.Tensor | None = None, out: torch
     return y, scale
 
 
-def pack_conv_weight(w: torch.Tensor, stream=None) -> torch.Tensor:
-    """Pack E4M3 conv weights [cout, cin, kh, kw] for conv2d."""
+def pack_conv_weight(w: torch.Tensor, group: int = 1, stream=None) -> torch.Tensor:
+    """Pack E4M3 conv weights [cout, cin/group, kh, kw] for conv2d."""
     assert w.dtype == torch.uint8 and w.is_contiguous() and w.dim() == 4
-    cout, cin, kh, kw = w.shape
-    p = torch.empty(packed_weight_bytes(kh * kw * cin, cout), dtype=torch.uint8, device=w.device)
-    _check(lib().lcml_fp8_pack_conv_weight(_ptr(w), cout, cin, kh, kw, _ptr(p), _stream(stream)))
+    cout, cin_g, kh, kw = w.shape
+    p = torch.empty(lib().lcml_fp8_packed_conv_weight_bytes(cout, cin_g, kh, kw, group), dtype=torch.uint8,
+                    device=w.device)
+    _check(lib().lcml_fp8_pack_conv_weight(_ptr(w), cout, cin_g, kh, kw, group, _ptr(p), _stream(stream)))
     return p
 
 
 def conv2d(x_nhwc: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
            cout: int, kernel_shape, strides=(1, 1), pads=(0, 0), dilations=(1, 1), out_hw=None,
            bias: torch.Tensor | None = None, act: int = ACT_NONE, out_dtype=torch.float32,
-           kernel: int = KERNEL_AUTO, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+           kernel: int = KERNEL_AUTO, out: torch.Tensor | None = None, group: int = 1,
+           stream=None) -> torch.Tensor:
     """FP8 conv (implicit im2col on the matrix cores): NHWC E4M3 in, NCHW out.
     pads are begin pads; out_hw defaults to symmetric padding."""
     n, h, w, c = x_nhwc.shape
@@ -289,7 +292,7 @@ def conv2d(x_nhwc: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, 
     per_ch = int(w_scale.numel() > 1)
     _check(lib().lcml_fp8_conv2d(_ptr(x_nhwc), _ptr(x_scale), n, c, h, w, _ptr(w_packed), _ptr(w_scale), per_ch,
                                  cout, kh, kw, strides[0], strides[1], pads[0], pads[1], dilations[0], dilations[1],
-                                 1, oh, ow, _ptr(bias), int(act), _ptr(y), _DTYPE_CODE.get(y.dtype, 0), int(kernel),
+                                 group, oh, ow, _ptr(bias), int(act), _ptr(y), _DTYPE_CODE.get(y.dtype, 0), int(kernel),
                                  _stream(stream)))
     return y
 

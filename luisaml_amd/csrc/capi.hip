@@ -268,13 +268,21 @@ int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64_t c, int
     return hip_status(err, fn);
 }
 
-int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin, int64_t kh, int64_t kw, uint8_t *packed,
-                              void *stream) {
+int64_t lcml_fp8_packed_conv_weight_bytes(int64_t cout, int64_t cin_g, int64_t kh, int64_t kw, int64_t group) {
+    if (cout <= 0 || cin_g <= 0 || kh <= 0 || kw <= 0 || group <= 0 || cout % group != 0) return 0;
+    return group * lcml_fp8_packed_weight_bytes(kh * kw * cin_g, cout / group);
+}
+
+int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t cin_g, int64_t kh, int64_t kw, int64_t group,
+                              uint8_t *packed, void *stream) {
     const char *fn = "lcml_fp8_pack_conv_weight";
-    if (cout <= 0 || cin <= 0 || kh <= 0 || kw <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: bad shape", fn);
+    if (cout <= 0 || cin_g <= 0 || kh <= 0 || kw <= 0 || group <= 0 || cout % group != 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: bad shape or group", fn);
     if (!w || !packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
     if (!aligned(packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: packed not 16-byte aligned", fn);
-    return hip_status(lcml::launch_pack_conv_weight(w, (int)cout, (int)cin, (int)kh, (int)kw, packed,
+    if (lcml_fp8_packed_conv_weight_bytes(cout, cin_g, kh, kw, group) >= (int64_t)1 << 31)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: packed weight larger than 2 GiB", fn);
+    return hip_status(lcml::launch_pack_conv_weight(w, (int)cout, (int)cin_g, (int)kh, (int)kw, (int)group, packed,
                                                     (hipStream_t)stream),
                       fn);
 }
@@ -289,11 +297,15 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
         return fail(LCML_ERR_INVALID_ARG, "%s: bad shape", fn);
     if (stride_h <= 0 || stride_w <= 0 || dil_h <= 0 || dil_w <= 0 || pad_h < 0 || pad_w < 0)
         return fail(LCML_ERR_INVALID_ARG, "%s: strides and dilations must be >= 1, pads >= 0", fn);
-    if (group != 1) return fail(LCML_ERR_UNSUPPORTED, "%s: group=%lld (only 1 is implemented)", fn, (long long)group);
-    if (c % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: c=%lld is not a multiple of 16", fn, (long long)c);
-    const int64_t M = n * oh * ow, K = kh * kw * c;
+    if (group <= 0 || c % group != 0 || cout % group != 0)
+        return fail(LCML_ERR_INVALID_ARG, "%s: group=%lld must divide c=%lld and cout=%lld", fn, (long long)group,
+                    (long long)c, (long long)cout);
+    if ((c / group) % 16 != 0)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: channels per group (%lld) not a multiple of 16", fn,
+                    (long long)(c / group));
+    const int64_t M = n * oh * ow;
     if (n * h * w * c >= (int64_t)1 << 31 || M >= (int64_t)1 << 31 ||
-        lcml_fp8_packed_weight_bytes(K, cout) >= (int64_t)1 << 31)
+        lcml_fp8_packed_conv_weight_bytes(cout, c / group, kh, kw, group) >= (int64_t)1 << 31)
         return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB", fn);
     if (kernel == LCML_KERNEL_AUTO) kernel = LCML_KERNEL_MFMA;
     if (kernel != LCML_KERNEL_MFMA && kernel != LCML_KERNEL_MFMA_FP8)
@@ -302,13 +314,17 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
     if (int rc = make_epilogue(e, fn, M, cout, x_scale, w_scale, w_scale_per_channel, 1.0f, bias, 1, cout, 0, 1.0f,
                                act, y, y_dtype, cout))
         return rc;
+    // per group: N = cout/group columns; the scale and bias pointers are
+    // advanced to the group's channels in the kernel
+    e.N = cout / group;
+    e.c0 = cout / group;
     if (n == 0) return LCML_OK;
     if (!x_nhwc || !w_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
     if (!aligned(x_nhwc, 16) || !aligned(w_packed, 16))
         return fail(LCML_ERR_INVALID_ARG, "%s: x_nhwc and w_packed must be 16-byte aligned", fn);
     return hip_status(lcml::launch_conv_mfma(x_nhwc, n, (int)c, (int)h, (int)w, w_packed, (int)cout, (int)kh, (int)kw,
                                              (int)stride_h, (int)stride_w, (int)pad_h, (int)pad_w, (int)dil_h,
-                                             (int)dil_w, (int)oh, (int)ow, e, kernel == LCML_KERNEL_MFMA,
+                                             (int)dil_w, (int)group, (int)oh, (int)ow, e, kernel == LCML_KERNEL_MFMA,
                                              (hipStream_t)stream),
                       fn);
 }

@@ -51,26 +51,28 @@ __global__ __launch_bounds__(kThreads) void k_quantize_nchw_to_nhwc(const float 
     }
 }
 
-// One thread per 16-byte unit of the packed matrix (16 consecutive k of one
-// column n): k = (kh*KW + kw)*Cin + c gathers W[n][c][kh][kw]; k >= K and
-// n >= Cout are zero.
-__global__ void k_pack_conv_weight(const uint8_t *__restrict__ w, int Cout, int Cin, int KH, int KW,
-                                   uint8_t *__restrict__ packed, int64_t KC, int64_t units) {
+// One thread per 16-byte unit of the packed matrices (16 consecutive k of
+// one column n of one group's GEMM weight): k = (kh*KW + kw)*Cin + c gathers
+// W[grp*Mg + n][c][kh][kw]; k >= K and n >= Mg are zero.
+__global__ void k_pack_conv_weight(const uint8_t *__restrict__ w, int Mg, int Cin, int KH, int KW,
+                                   uint8_t *__restrict__ packed, int64_t KC, int64_t units_g, int64_t units) {
     const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (u >= units) return;
+    const int64_t grp = u / units_g, ul = u - grp * units_g;
     // packed byte (k, n) sits at ((n/64)*KC + k/16)*1024 + (n%64)*16 + k%16
-    const int64_t blk = u / 64, col = u - blk * 64;  // 1 KB block = 64 columns x 16 k
+    const int64_t blk = ul / 64, col = ul - blk * 64;  // 1 KB block = 64 columns x 16 k
     const int64_t panel = blk / KC, kc = blk - panel * KC;
     const int64_t n = panel * 64 + col;
     const int64_t K = (int64_t)KH * KW * Cin;
     uint32_t out[4] = {0u, 0u, 0u, 0u};
-    if (n < Cout) {
+    if (n < Mg) {
+        const int64_t co = grp * Mg + n;
         for (int j = 0; j < 16; ++j) {
             const int64_t k = kc * 16 + j;
             if (k >= K) break;
             const int64_t tap = k / Cin, c = k - tap * Cin;
             const int64_t kh = tap / KW, kw = tap - kh * KW;
-            const uint32_t b = w[((n * Cin + c) * KH + kh) * KW + kw];
+            const uint32_t b = w[((co * Cin + c) * KH + kh) * KW + kw];
             out[j >> 2] |= b << (8 * (j & 3));
         }
     }
@@ -92,13 +94,14 @@ hipError_t launch_quantize_nhwc(const float *x, uint8_t *y, int64_t Nb, int C, i
     return hipGetLastError();
 }
 
-hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin, int KH, int KW, uint8_t *packed,
+hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin_g, int KH, int KW, int group, uint8_t *packed,
                                    hipStream_t s) {
-    const int64_t K = (int64_t)KH * KW * Cin;
-    const int64_t KC = pad_to(K, kPackK) / 16, npanels = pad_to(Cout, kPanelCols) / 64;
-    const int64_t units = npanels * KC * 64;
-    hipLaunchKernelGGL(k_pack_conv_weight, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, w, Cout, Cin, KH,
-                       KW, packed, KC, units);
+    const int Mg = Cout / group;
+    const int64_t K = (int64_t)KH * KW * Cin_g;
+    const int64_t KC = pad_to(K, kPackK) / 16, npanels = pad_to(Mg, kPanelCols) / 64;
+    const int64_t units_g = npanels * KC * 64, units = units_g * group;
+    hipLaunchKernelGGL(k_pack_conv_weight, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, w, Mg, Cin_g, KH,
+                       KW, packed, KC, units_g, units);
     return hipGetLastError();
 }
 

@@ -93,8 +93,11 @@ struct Tile {
 // and taps that fall into the padding read zeros (the reference's unsigned
 // bounds check, conv.cpp:145-148; begin pads only, conv.cpp:121).  The
 // output goes to NCHW: Y[n][co][oh][ow].
+// With groups, workgroup row blockIdx.y = g runs the GEMM of group g: input
+// channels g*Cg .. (g+1)*Cg-1, output channels g*N .. (g+1)*N-1 (N = Cout /
+// group), weights = the g-th packed block.
 struct ConvGeom {
-    int H, W, C, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw;
+    int H, W, Cg, Ctot, CoutTot, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw;
 };
 
 struct GemmArgs {
@@ -151,8 +154,9 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     // k-chunk b%CPR of the step.
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, (int)g.a_bytes, 0x00020000);
+    const int grp = CONV ? (int)blockIdx.y : 0;  // CONV: convolution group
     const __amdgpu_buffer_rsrc_t b_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void *)g.bp, 0, (int)g.b_bytes, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)(g.bp + (size_t)grp * g.b_bytes), 0, (int)g.b_bytes, 0x00020000);
     uint32_t a_off[T::A_BLK];
     int a_kc[T::A_BLK];
     uint32_t b_off[T::B_BLK];
@@ -172,14 +176,14 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             const uint32_t ohw = (uint32_t)(cv.OH * cv.OW);
             const uint32_t mm = m < g.M ? (uint32_t)m : 0u;
             const uint32_t n = mm / ohw, pix = mm - n * ohw, oh = pix / (uint32_t)cv.OW, ow = pix - oh * (uint32_t)cv.OW;
-            a_off[i] = n * (uint32_t)(cv.H * cv.W * cv.C);
+            a_off[i] = n * (uint32_t)(cv.H * cv.W * cv.Ctot) + (uint32_t)(grp * cv.Cg);
             a_ih0[i] = m < g.M ? (int)oh * cv.sh - cv.ph : -(1 << 30);
             a_iw0[i] = (int)ow * cv.sw - cv.pw;
             // step 0 starts at k = c*16 < 64 <= ... ; c*16 may still exceed C
             // (C >= 16), so normalise once
             int cc = c * 16, kw = 0, kh = 0;
-            while (cc >= cv.C) {
-                cc -= cv.C;
+            while (cc >= cv.Cg) {
+                cc -= cv.Cg;
                 if (++kw == cv.KW) { kw = 0; ++kh; }
             }
             a_c[i] = cc; a_kw[i] = kw; a_kh[i] = kh;
@@ -207,11 +211,12 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 const uint32_t k = kbyte + (uint32_t)a_kc[i];
                 const int ih = a_ih0[i] + a_kh[i] * cv.dh, iw = a_iw0[i] + a_kw[i] * cv.dw;
                 const bool ok = (int64_t)k < g.K && (uint32_t)ih < (uint32_t)cv.H && (uint32_t)iw < (uint32_t)cv.W;
-                off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.C + (uint32_t)a_c[i]
+                off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.Ctot +
+                               (uint32_t)a_c[i]
                          : OOB;
                 a_c[i] += BK;
-                while (a_c[i] >= cv.C) {
-                    a_c[i] -= cv.C;
+                while (a_c[i] >= cv.Cg) {
+                    a_c[i] -= cv.Cg;
                     if (++a_kw[i] == cv.KW) { a_kw[i] = 0; ++a_kh[i]; }
                 }
             } else {
@@ -362,7 +367,11 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     // as one rolled loop with a fixed column per lane instead of unrolled
     // copies of the activation code.  Row pitch 33 floats keeps the
     // 2-row-per-instruction writes conflict free.
-    const Epilogue &e = g.e;
+    Epilogue e = g.e;
+    if (CONV && grp) {  // this group's output channels
+        if (e.b_scale && e.b_per_channel) e.b_scale += (int64_t)grp * e.N;
+        if (e.c) e.c += (int64_t)grp * e.N;
+    }
     const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
     float *st = reinterpret_cast<float *>(smem) + wave * (WM * 32 * EP_PITCH);
 #pragma unroll
@@ -383,7 +392,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 const int64_t m = m0 + wm * WM * 32 + rl;
                 if (m < e.M) {
                     const uint32_t n = (uint32_t)m / ohw, pix = (uint32_t)m - n * ohw;
-                    const int64_t ybase = (int64_t)n * e.N * ohw + pix;
+                    const int64_t ybase = ((int64_t)n * g.cv.CoutTot + (int64_t)grp * e.N) * ohw + pix;
 #pragma unroll 1
                     for (int c = 0; c < 32; ++c) {
                         const int64_t col = n0 + wn * WN * 32 + j * 32 + c;
@@ -442,7 +451,8 @@ hipError_t launch(GemmArgs &g, hipStream_t s) {
     g.tiles_n = (int)((g.N + Shipped::BN - 1) / Shipped::BN);
     g.nk = (int)(Kp / BK);
     g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
-    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n), dim3(Shipped::NT), Shipped::LDS_BYTES, s, g);
+    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Shipped::NT),
+                       Shipped::LDS_BYTES, s, g);
     return hipGetLastError();
 }
 
@@ -458,11 +468,12 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
 }
 
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
-                            int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int OH, int OW,
+                            int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int group, int OH, int OW,
                             const Epilogue &e, bool exact, hipStream_t s) {
     GemmArgs g = {};
-    g.cv = ConvGeom{H, W, C, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw};
-    g.M = Nb * OH * OW; g.N = Cout; g.K = (int64_t)KH * KW * C;
+    const int Cg = C / group;
+    g.cv = ConvGeom{H, W, Cg, C, Cout, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw};
+    g.M = Nb * OH * OW; g.N = Cout / group; g.K = (int64_t)KH * KW * Cg;
     g.a = x_nhwc; g.lda = 0; g.bp = bp;
     g.a_bytes = (uint32_t)(Nb * H * W * C);
     g.e = e;

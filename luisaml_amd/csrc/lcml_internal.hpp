@@ -29,16 +29,20 @@ hipError_t launch_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                             const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
 // implicit-im2col FP8 convolution on the MFMA tile kernel: x_nhwc E4M3
-// [Nb][H][W][C] (C % 16 == 0), bp = conv weights packed with K = (kh, kw, c),
-// output NCHW [Nb][Cout][OH][OW] through the epilogue (y, y_bf16; ldy unused)
+// [Nb][H][W][C] ((C/group) % 16 == 0), bp = conv weights packed per group
+// with K = (kh, kw, c), output NCHW [Nb][Cout][OH][OW] through the epilogue
+// (y, y_bf16; ldy unused; the epilogue's N is Cout/group and its per-channel
+// scale and bias pointers cover all Cout channels)
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
-                            int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int OH, int OW,
+                            int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int group, int OH, int OW,
                             const Epilogue &e, bool exact, hipStream_t s);
 // NCHW fp32 -> NHWC E4M3 with a per-tensor scale: scale[0], or amax/448 from
 // *amax_bits when amax_bits is given (then written to scale_out if non-null)
 hipError_t launch_quantize_nhwc(const float *x, uint8_t *y, int64_t Nb, int C, int H, int W, const float *scale,
                                 const uint32_t *amax_bits, float *scale_out, hipStream_t s);
-hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin, int KH, int KW, uint8_t *packed,
+// per group g: the packed GEMM weight of W[g*Cout/group ..][Cin_g][KH][KW],
+// blocks of packed_weight_bytes(KH*KW*Cin_g, Cout/group) one after another
+hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin_g, int KH, int KW, int group, uint8_t *packed,
                                    hipStream_t s);
 hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                               const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);

@@ -115,8 +115,8 @@ void NetworkInstance::create_tensor_for_var(const Variable &var) {
 // [x -> DynamicQuantizeLinear -> DequantizeLinear] or plain fp32 A, and
 // DequantizeLinear(W_e4m3 constant, s_w) as B, into Gemm/MatMul, optionally
 // followed by Relu/Gelu, become one FP8Linear node; the same with a quantised
-// activation into Conv (4-D E4M3 weight, group 1, cin % 16 == 0) becomes one
-// FP8Conv node.
+// activation into Conv (4-D E4M3 weight, channels per group % 16 == 0)
+// becomes one FP8Conv node.
 // ------------------------------------------------------------------------
 namespace {
 
@@ -230,9 +230,8 @@ void NetworkInstance::fuse_qdq_linear() {
         const Node &n = nodes[i];
         if (n.get_op_type() == "Conv") {
             // ---- DQ(x) , DQ(W_e4m3 [cout, cin, kh, kw]) -> Conv [-> act] ----
-            if (n.get_inputs().size() < 2 || attr_int(n, "group", 1) != 1 ||
-                attr_string(n, "auto_pad", "NOTSET") != "NOTSET")
-                continue;
+            const int group = attr_int(n, "group", 1);
+            if (n.get_inputs().size() < 2 || group < 1 || attr_string(n, "auto_pad", "NOTSET") != "NOTSET") continue;
             const Variable &X = n.get_inputs()[0].get();
             const Variable &Bv = n.get_inputs()[1].get();
             const Node *dqw = match_weight(Bv, i, 4);
@@ -240,10 +239,10 @@ void NetworkInstance::fuse_qdq_linear() {
             const Variable &W = dqw->get_inputs()[0].get();
             const Variable &sw = dqw->get_inputs()[1].get();
             const auto &ws = W.get_shape();
-            const size_t cout = ws[0], cin = ws[1], kh = ws[2], kw = ws[3];
-            if (cin % 16 != 0) continue;
+            const size_t cout = ws[0], cin = ws[1], kh = ws[2], kw = ws[3];  // cin: channels per group
+            if (cin % 16 != 0 || cout % (size_t)group != 0) continue;
             if (sw.num_elements() != 1 && !(sw.num_elements() == cout && attr_int(*dqw, "axis", 1) == 0)) continue;
-            if (X.get_shape().size() != 4 || X.get_shape()[1] != cin) continue;
+            if (X.get_shape().size() != 4 || X.get_shape()[1] != cin * (size_t)group) continue;
             ActQ aq = match_act(X, i);
             if (aq.a_mode == 0) continue;  // FP8 conv needs a quantised activation
             std::vector<size_t> drop = aq.drop;
@@ -264,7 +263,7 @@ void NetworkInstance::fuse_qdq_linear() {
             const bool has_bias = n.get_inputs().size() > 2;
             if (has_bias) f.add_input(n.get_inputs()[2].get());
             f.add_output(*out);
-            for (const char *a : {"strides", "pads", "dilations"})
+            for (const char *a : {"strides", "pads", "dilations", "group"})
                 if (auto *at = n.try_get_attr(a)) f.set_attribute(*at);
             f.set_attribute(Attribute{"kernel_shape", std::vector<int32_t>{(int32_t)kh, (int32_t)kw}});
             f.set_attribute(Attribute{"a_mode", (int32_t)aq.a_mode});
@@ -356,11 +355,14 @@ void NetworkInstance::pack_weights() {
         create_tensor_for_var(W);
         create_tensor_for_var(sw);
         const uint32_t K = (uint32_t)pv.get_shape()[0], N = (uint32_t)pv.get_shape()[1];
-        DeviceArray<uint8_t> packed((size_t)lcml_fp8_packed_weight_bytes(K, N));
+        const auto &ws = W.get_shape();
+        const int64_t group = conv ? attr_int(n, "group", 1) : 1;
+        DeviceArray<uint8_t> packed(conv ? (size_t)lcml_fp8_packed_conv_weight_bytes(ws[0], ws[1], ws[2], ws[3], group)
+                                         : (size_t)lcml_fp8_packed_weight_bytes(K, N));
         ITensor &wt = table_.at(W.get_name());
         if (conv)
-            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), wt.shape(0),
-                                                 wt.shape(1), wt.shape(2), wt.shape(3), packed.data(), stream_),
+            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), ws[0], ws[1], ws[2],
+                                                 ws[3], group, packed.data(), stream_),
                        "pack conv weight");
         else
             lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,

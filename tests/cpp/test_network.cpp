@@ -377,12 +377,13 @@ static void test_dynamic_qdq_matmul() {
 // axis 0), B) -> Relu, fused into FP8Conv and op by op (fp32 Conv), both
 // against the oracle's direct conv of the dequantised operands; then an fp32
 // grouped Conv on its own.
-static void test_qdq_conv(bool fused) {
-    std::printf("[7] DynamicQuantizeLinear -> DQ -> Conv(DQ(W), B) -> Relu (%s)\n", fused ? "fused" : "op by op");
-    const int64_t Nb = 2, C = 32, H = 9, W = 11, CO = 24, KH = 3, KW = 3, OH = 9, OW = 11;
-    auto x = normals(71, (size_t)(Nb * C * H * W), 1.0f), w = normals(72, (size_t)(CO * C * KH * KW), 0.05f);
+static void test_qdq_conv(bool fused, int64_t G = 1) {
+    std::printf("[7] DynamicQuantizeLinear -> DQ -> Conv(DQ(W), B, group %lld) -> Relu (%s)\n", (long long)G,
+                fused ? "fused" : "op by op");
+    const int64_t Nb = 2, C = 32 * G, H = 9, W = 11, CO = 24, KH = 3, KW = 3, OH = 9, OW = 11, CG = C / G;
+    auto x = normals(71, (size_t)(Nb * C * H * W), 1.0f), w = normals(72, (size_t)(CO * CG * KH * KW), 0.05f);
     auto bias = normals(73, (size_t)CO, 0.01f);
-    const int64_t kper = C * KH * KW;
+    const int64_t kper = CG * KH * KW;
     std::vector<float> sw(CO, 0.0f);
     for (int64_t o = 0; o < CO; ++o)
         for (int64_t k = 0; k < kper; ++k) sw[o] = std::max(sw[o], std::fabs(w[o * kper + k]));
@@ -392,7 +393,7 @@ static void test_qdq_conv(bool fused) {
     Graph g("conv");
     Blob blob;
     var(g, "x", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
-    blob_var(g, blob, "W", DataType::FLOAT8E4M3FN, {(size_t)CO, (size_t)C, (size_t)KH, (size_t)KW}, qw.data(),
+    blob_var(g, blob, "W", DataType::FLOAT8E4M3FN, {(size_t)CO, (size_t)CG, (size_t)KH, (size_t)KW}, qw.data(),
              qw.size());
     blob_var(g, blob, "sw", DataType::FLOAT, {(size_t)CO}, sw.data(), CO * 4);
     blob_var(g, blob, "B", DataType::FLOAT, {(size_t)CO}, bias.data(), CO * 4);
@@ -400,14 +401,15 @@ static void test_qdq_conv(bool fused) {
     var(g, "xs", DataType::FLOAT, {1});
     var(g, "xz", DataType::FLOAT8E4M3FN, {1});
     var(g, "xd", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
-    var(g, "Wf", DataType::FLOAT, {(size_t)CO, (size_t)C, (size_t)KH, (size_t)KW});
+    var(g, "Wf", DataType::FLOAT, {(size_t)CO, (size_t)CG, (size_t)KH, (size_t)KW});
     var(g, "c", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
     var(g, "y", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
     node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
     node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
     node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"}, {Attribute{"axis", (int32_t)0}});
     node(g, "Conv", {"xd", "Wf", "B"}, {"c"},
-         {Attribute{"kernel_shape", std::vector<int32_t>{3, 3}}, Attribute{"pads", std::vector<int32_t>{1, 1, 1, 1}}});
+         {Attribute{"kernel_shape", std::vector<int32_t>{3, 3}}, Attribute{"pads", std::vector<int32_t>{1, 1, 1, 1}},
+          Attribute{"group", (int32_t)G}});
     node(g, "Relu", {"c"}, {"y"});
     g.add_input("x");
     g.add_output("y");
@@ -434,13 +436,13 @@ static void test_qdq_conv(bool fused) {
     std::vector<float> A(x.size()), Bw(w.size()), ref(y.size()), absA(x.size()), absB(w.size()), bnd(y.size());
     orc_dequantize(qx.data(), A.data(), 1, 1, qx.size(), &sx);
     orc_dequantize(qw.data(), Bw.data(), 1, CO, kper, sw.data());
-    orc_conv2d(A.data(), Bw.data(), bias.data(), ref.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, 1, OH, OW,
+    orc_conv2d(A.data(), Bw.data(), bias.data(), ref.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, G, OH, OW,
                LCML_ACT_RELU);
     for (size_t i = 0; i < A.size(); ++i) absA[i] = std::fabs(A[i]);
     for (size_t i = 0; i < Bw.size(); ++i) absB[i] = std::fabs(Bw[i]);
     std::vector<float> absb(bias.size());
     for (size_t i = 0; i < bias.size(); ++i) absb[i] = std::fabs(bias[i]);
-    orc_conv2d(absA.data(), absB.data(), absb.data(), bnd.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, 1, OH, OW,
+    orc_conv2d(absA.data(), absB.data(), absb.data(), bnd.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, G, OH, OW,
                LCML_ACT_NONE);
     std::vector<double> bound(bnd.begin(), bnd.end());
     CHECK(close(y, ref, bound, 1e-4, 0.0, fused ? "fused qdq conv" : "qdq conv op by op"));
@@ -588,6 +590,7 @@ int main(int argc, char **argv) {
         test_standalone_qdq_cast();
         test_qdq_conv(true);
         test_qdq_conv(false);
+        test_qdq_conv(true, 2);
         test_f32_grouped_conv();
         test_errors();
     } catch (const Error &e) {

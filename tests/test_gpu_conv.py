@@ -22,9 +22,9 @@ def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def conv_case(n, c, h, w, cout, kh, kw, seed, dev, per_channel=True):
+def conv_case(n, c, h, w, cout, kh, kw, seed, dev, per_channel=True, group=1):
     x = synth.normal(seed, (n, c, h, w))
-    wt = synth.normal(seed + 1, (cout, c, kh, kw), std=0.03)
+    wt = synth.normal(seed + 1, (cout, c // group, kh, kw), std=0.03)
     ws = oracle.channel_scales(wt.reshape(cout, -1), 0) if per_channel else \
         np.array([oracle.dynamic_scale(wt)], np.float32)
     qw = oracle.quantize(wt.reshape(cout, -1), ws, axis=0).reshape(wt.shape) if per_channel else \
@@ -58,6 +58,18 @@ def test_pack_conv_weight_layout(dev, cout, cin, kh, kw):
     K = kh * kw * cin
     back = capi.unpack_weight(p, K, cout, w_is_nk=True).cpu().numpy()  # [cout, K]
     assert np.array_equal(back, q.transpose(0, 2, 3, 1).reshape(cout, K))
+    # grouped: block g is group g's [K_g, cout/group] packed weight
+    for group in (2, 4):
+        if cout % group or cin % group:
+            continue
+        qg = np.ascontiguousarray(q[:, : cin // group])
+        pg = capi.pack_conv_weight(to_dev(qg, dev), group=group)
+        Kg, Mg = kh * kw * (cin // group), cout // group
+        gb = capi.packed_weight_bytes(Kg, Mg)
+        assert pg.numel() == group * gb
+        for gi in range(group):
+            back = capi.unpack_weight(pg[gi * gb:(gi + 1) * gb], Kg, Mg, w_is_nk=True).cpu().numpy()
+            assert np.array_equal(back, qg[gi * Mg:(gi + 1) * Mg].transpose(0, 2, 3, 1).reshape(Mg, Kg))
 
 
 CASES = [  # n, c, h, w, cout, kh, kw, stride, pad, dilation
@@ -71,7 +83,7 @@ CASES = [  # n, c, h, w, cout, kh, kw, stride, pad, dilation
 ]
 
 
-def reference(x, qw, ws, bias, stride, pad, dil, act, per_channel=True):
+def reference(x, qw, ws, bias, stride, pad, dil, act, per_channel=True, group=1):
     s = np.float32(oracle.dynamic_scale(x))
     xq = oracle.quantize(x, s)
     A = oracle.dequantize(xq, s)
@@ -79,9 +91,9 @@ def reference(x, qw, ws, bias, stride, pad, dil, act, per_channel=True):
     B = oracle.dequantize(qw.reshape(cout, -1), ws, axis=0).reshape(qw.shape) if ws.size > 1 else \
         oracle.dequantize(qw, ws)
     st, pd, dl = (stride, stride), (pad, pad), (dil, dil)
-    Y = oracle.conv2d(A, B, bias, strides=st, pads=pd, dilations=dl, act=act)
+    Y = oracle.conv2d(A, B, bias, strides=st, pads=pd, dilations=dl, group=group, act=act)
     bound = oracle.conv2d(np.abs(A), np.abs(B), None if bias is None else np.abs(bias), strides=st, pads=pd,
-                          dilations=dl)
+                          dilations=dl, group=group)
     return Y, bound
 
 
@@ -97,6 +109,27 @@ def test_conv_matches_oracle(dev, case, act):
     ref, bound = reference(x, qw, ws, bias, stride, pad, dil, act)
     assert y.shape == ref.shape
     assert_close(y.cpu().numpy(), ref, bound, act=act)
+
+
+@pytest.mark.parametrize("case", [(2, 32, 9, 11, 24, 3, 3, 1, 1, 1, 2), (1, 64, 10, 10, 64, 3, 3, 2, 1, 1, 4),
+                                  (1, 48, 8, 8, 30, 1, 1, 1, 0, 1, 3), (2, 128, 7, 7, 256, 3, 3, 1, 2, 2, 8)])
+@pytest.mark.parametrize("kernel", [capi.KERNEL_MFMA, capi.KERNEL_MFMA_FP8])
+def test_grouped_conv_matches_oracle(dev, case, kernel):
+    """Grouped FP8 conv: each group's GEMM reads its channel slice and writes
+    its output-channel slice (conv.cpp:139,158)."""
+    n, c, h, w, cout, kh, kw, stride, pad, dil, group = case
+    x, qw, ws = conv_case(n, c, h, w, cout, kh, kw, seed=c + cout + group, dev=dev, group=group)
+    bias = synth.normal(78, (cout,), std=0.01)
+    xq, sx = capi.quantize_nhwc(to_dev(x, dev))
+    y = capi.conv2d(xq, sx, capi.pack_conv_weight(to_dev(qw, dev), group=group), to_dev(ws, dev), cout, (kh, kw),
+                    (stride, stride), (pad, pad), (dil, dil), bias=to_dev(bias, dev), act=capi.ACT_RELU,
+                    kernel=kernel, group=group)
+    ref, bound = reference(x, qw, ws, bias, stride, pad, dil, capi.ACT_RELU, group=group)
+    if kernel == capi.KERNEL_MFMA:
+        assert_close(y.cpu().numpy(), ref, bound, act=capi.ACT_RELU)
+    else:
+        rel = np.linalg.norm(y.cpu().numpy() - ref) / np.linalg.norm(ref)
+        assert rel < 3e-5
 
 
 def test_conv_bf16_out_and_per_tensor_weight_scale(dev):
@@ -128,6 +161,12 @@ def test_conv_errors(dev):
     bp = capi.pack_conv_weight(torch.zeros((4, 8, 3, 3), dtype=torch.uint8, device=dev))
     with pytest.raises(capi.LcmlError):
         capi.conv2d(xq, s, bp, s, 4, (3, 3), pads=(1, 1))
+    xq = torch.zeros((1, 4, 4, 32), dtype=torch.uint8, device=dev)  # 32 channels in 4 groups: 8 per group
+    bp = capi.pack_conv_weight(torch.zeros((8, 8, 3, 3), dtype=torch.uint8, device=dev), group=4)
+    with pytest.raises(capi.LcmlError):
+        capi.conv2d(xq, s, bp, s, 8, (3, 3), pads=(1, 1), group=4)
+    with pytest.raises(capi.LcmlError):  # group must divide cout
+        capi.conv2d(xq, s, bp, s, 6, (3, 3), pads=(1, 1), group=4)
 
 
 @pytest.mark.parametrize("case", [(2, 6, 9, 11, 8, 3, 3, 1, 1, 1, 1), (1, 8, 12, 12, 12, 3, 3, 2, 1, 1, 2),
