@@ -7,7 +7,18 @@ Box-Muller in double precision, rounded once to fp32.  Seeds are per
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
+
+
+def _threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n)), 16))
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -29,18 +40,43 @@ def uniform01(seed: int, n: int) -> np.ndarray:
     return (r >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
 
 
+def _uniform01_range(seed: int, first: int, count: int) -> np.ndarray:
+    """Elements first .. first+count-1 of uniform01(seed, .)."""
+    with np.errstate(over="ignore"):
+        base = np.uint64(seed) * np.uint64(0x100000001B3) + np.uint64(first)
+        ctr = np.arange(count, dtype=np.uint64) + base
+    r = _splitmix64(ctr)
+    return (r >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+_CHUNK = 1 << 20  # pairs per chunk: keeps the double temporaries cache-sized
+
+
 def normal(seed: int, shape, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
-    """fp32 N(mean, std^2) via Box-Muller in double."""
+    """fp32 N(mean, std^2) via Box-Muller in double (element 2i from the
+    cosine and 2i+1 from the sine of pair i), generated chunk by chunk."""
     n = int(np.prod(shape)) if len(shape) else 1
     m = (n + 1) // 2
-    u = uniform01(seed, 2 * m)
-    u1 = 1.0 - u[0::2]  # (0, 1]
-    u2 = u[1::2]
-    r = np.sqrt(-2.0 * np.log(u1))
-    z = np.empty(2 * m, np.float64)
-    z[0::2] = r * np.cos(2.0 * np.pi * u2)
-    z[1::2] = r * np.sin(2.0 * np.pi * u2)
-    return (z[:n] * std + mean).astype(np.float32).reshape(shape)
+    out = np.empty(2 * m, np.float32)
+
+    def chunk(p0):
+        pc = min(_CHUNK, m - p0)
+        u = _uniform01_range(seed, 2 * p0, 2 * pc)
+        u1 = 1.0 - u[0::2]  # (0, 1]
+        u2 = u[1::2]
+        r = np.sqrt(-2.0 * np.log(u1))
+        z = np.empty(2 * pc, np.float64)
+        z[0::2] = r * np.cos(2.0 * np.pi * u2)
+        z[1::2] = r * np.sin(2.0 * np.pi * u2)
+        out[2 * p0:2 * (p0 + pc)] = (z * std + mean).astype(np.float32)
+
+    starts = range(0, m, _CHUNK)
+    if len(starts) > 1:  # numpy releases the GIL inside these ufuncs
+        with ThreadPoolExecutor(min(len(starts), _threads())) as ex:
+            list(ex.map(chunk, starts))
+    elif m:
+        chunk(0)
+    return out[:n].reshape(shape)
 
 
 def uniform(seed: int, shape, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:

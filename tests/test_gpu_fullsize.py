@@ -1,0 +1,116 @@
+"""Parity at the benchmarked sizes (the configurations bench.py measures).
+
+Same bars as the smaller parity tests: quantisation bit-exact, GEMM outputs
+elementwise within 1e-4 * sum|a*b| and relative Frobenius 1e-5 against the
+oracle's dequantise-then-Gemm / direct conv (reference gemm.cpp:27-325,
+conv.cpp:115-207).  Where the full oracle product would take minutes on the
+host, a fixed sample of output rows (or one image of the conv batch) is
+checked against the oracle; the GPU computes the full problem.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from luisaml_amd import capi, synth
+from tests.gemm_cases import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def per_channel_weight(w, dev):
+    """W [K, N] -> per-output-channel E4M3 (codes checked bit-exact)."""
+    sw = oracle.channel_scales(w, 1)
+    qw = oracle.quantize(w, sw, axis=1)
+    d_sw = to_dev(sw, dev)
+    q_dev = capi.quantize(to_dev(w, dev), d_sw, axis=1)
+    assert np.array_equal(q_dev.cpu().numpy(), qw)
+    return qw, sw, capi.pack_weight(q_dev, w_is_nk=False), d_sw
+
+
+@pytest.fixture(scope="module")
+def decode_weight(dev):
+    w = synth.normal(101, (4096, 11008), std=0.02)
+    return per_channel_weight(w, dev)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_small_m_decode_linear_full(dev, decode_weight, M):
+    """x[M,4096] fp32 N(0,1) -> dynamic E4M3 -> x W[4096,11008] (per-channel) -> bf16."""
+    qw, sw, bp, d_sw = decode_weight
+    x = synth.normal(200 + M, (M, 4096))
+    s_out = torch.empty(1, device=dev)
+    y = capi.gemm_dynamic(to_dev(x, dev), bp, d_sw, 11008, 4096, out_dtype=torch.float32, scale_out=s_out)
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    assert s_out.cpu().numpy().view(np.uint32)[0] == s_ref.view(np.uint32)
+    ref, A, B = oracle.qlinear(oracle.quantize(x, s_ref), s_ref, qw, sw)
+    assert_close(y.cpu().numpy(), ref, oracle.gemm_abs_bound(A, B))
+    y16 = capi.gemm_dynamic(to_dev(x, dev), bp, d_sw, 11008, 4096, out_dtype=torch.bfloat16)
+    assert np.array_equal(y16.view(torch.int16).cpu().numpy().view(np.uint16), oracle.bf16_rne(y.cpu().numpy()))
+
+
+ROWS = np.array([0, 1, 255, 256, 1023, 2048, 4095, 4096, 5000, 6143, 7777, 8191])
+
+
+def test_gemm_8192_cubed_sampled_rows(dev):
+    """8192^3, A and B from N(0,1) with per-tensor scales amax/448, bf16 out;
+    12 rows (tile edges included) against the oracle over all 8192 columns."""
+    n = 8192
+    a = synth.normal(301, (n, n))
+    b = synth.normal(302, (n, n))
+    qa, sa = capi.quantize_dynamic(to_dev(a, dev))
+    qb, sb = capi.quantize_dynamic(to_dev(b, dev))
+    sa_ref, sb_ref = np.float32(oracle.dynamic_scale(a)), np.float32(oracle.dynamic_scale(b))
+    assert float(sa.item()) == sa_ref and float(sb.item()) == sb_ref
+    bp = capi.pack_weight(qb, w_is_nk=False)
+    y = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.float32, kernel=capi.KERNEL_MFMA)
+    ys = y[torch.from_numpy(ROWS).to(dev)].cpu().numpy()
+    qa_rows = qa[torch.from_numpy(ROWS).to(dev)].cpu().numpy()
+    assert np.array_equal(qa_rows, oracle.quantize(a[ROWS], sa_ref))
+    qb_h = qb.cpu().numpy()
+    ref, A, B = oracle.qlinear(qa_rows, sa_ref, qb_h, sb_ref)
+    assert_close(ys, ref, oracle.gemm_abs_bound(A, B))
+
+
+def test_transformer_up_projection_gelu_sampled_rows(dev):
+    """M=4096 x 4096 -> 11008 with bias and GELU, dynamic activation scale,
+    per-channel weights (the up-projection of the transformer block)."""
+    x = synth.normal(420, (4096, 4096))
+    w = synth.normal(402, (4096, 11008), std=0.02)
+    bias = synth.normal(412, (11008,), std=0.01)
+    qw, sw, bp, d_sw = per_channel_weight(w, dev)
+    y = capi.gemm_dynamic(to_dev(x, dev), bp, d_sw, 11008, 4096, c=to_dev(bias, dev), act=capi.ACT_GELU_ERF,
+                          kernel=capi.KERNEL_MFMA)
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    rows = ROWS[ROWS < 4096]
+    ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw, bias=bias, act=oracle.ACT_GELU_ERF)
+    assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias),
+                 act=oracle.ACT_GELU_ERF)
+
+
+def test_conv3x3_resnet_one_image(dev):
+    """x[32,256,56,56] -> NHWC E4M3 (dynamic) -> 3x3 conv pad 1, 256 out,
+    per-channel weights, bias + ReLU; image 5 of the batch against the
+    oracle's direct conv."""
+    x = synth.normal(600, (32, 256, 56, 56))
+    w = synth.normal(601, (256, 256, 3, 3), std=0.03)
+    bias = synth.normal(602, (256,), std=0.01)
+    ws = oracle.channel_scales(w.reshape(256, -1), 0)
+    qw = oracle.quantize(w.reshape(256, -1), ws, axis=0).reshape(w.shape)
+    xq, sx = capi.quantize_nhwc(to_dev(x, dev))
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    assert float(sx.item()) == s_ref
+    y = capi.conv2d(xq, sx, capi.pack_conv_weight(to_dev(qw, dev)), to_dev(ws, dev), 256, (3, 3), pads=(1, 1),
+                    bias=to_dev(bias, dev), act=capi.ACT_RELU)
+    img = 5
+    xi = x[img:img + 1]
+    assert np.array_equal(xq[img].cpu().numpy(), oracle.quantize(xi, s_ref)[0].transpose(1, 2, 0))
+    A = oracle.dequantize(oracle.quantize(xi, s_ref), s_ref)
+    B = oracle.dequantize(qw.reshape(256, -1), ws, axis=0).reshape(qw.shape)
+    ref = oracle.conv2d(A, B, bias, pads=(1, 1), act=oracle.ACT_RELU)
+    bound = oracle.conv2d(np.abs(A), np.abs(B), np.abs(bias), pads=(1, 1))
+    assert_close(y[img:img + 1].cpu().numpy(), ref, bound, act=oracle.ACT_RELU)
