@@ -241,7 +241,26 @@ def main() -> int:
         b = torch.from_numpy(synth.normal(302, (BIG, BIG))).to(dev)  # [K, N]
         qa, sa = capi.quantize_dynamic(a)
         qb, sb = capi.quantize_dynamic(b)
-        del a, b
+        # the standalone Q / DQ kernels on one 8192^2 operand (67.1M elements,
+        # 5 algorithmic bytes each: fp32 one way, E4M3 the other)
+        nq = BIG * BIG
+        q_out = torch.empty_like(qa)
+        ws_q = torch.empty(capi.DYNAMIC_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
+        s_q = torch.empty(1, dtype=torch.float32, device=dev)
+        qkern = {}
+        for name, fn in (("quantize_static", lambda: capi.quantize(a, sa, out=q_out)),
+                         ("quantize_dynamic", lambda: capi.quantize_dynamic(a, out=q_out, scale_out=s_q,
+                                                                            workspace=ws_q)),
+                         ("dequantize", lambda: capi.dequantize(qa, sa, out=b))):
+            fn()
+            n = max(5, args.steps)
+            ms = timed(lambda: [fn() for _ in range(n)]) / n
+            gbs = 5.0 * nq / (ms * 1e-3) / 1e9
+            qkern[name] = {"ms": round(ms, 4), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        qkern["quantize_dynamic"]["note"] = "two passes over x (amax partials, then encode): 9 B/elem moved"
+        out["quantize_kernels_67m"] = {"workload": "8192x8192 fp32 N(0,1) <-> E4M3, per-tensor scale",
+                                       "elements": nq, "bytes_per_element": 5, **qkern}
+        del a, b, q_out
         bp = capi.pack_weight(qb, w_is_nk=False)
         del qb
         y = torch.empty((BIG, BIG), dtype=torch.bfloat16, device=dev)

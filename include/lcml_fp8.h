@@ -38,7 +38,8 @@ extern "C" {
 #define LCML_API
 #endif
 
-#define LCML_FP8_ABI_VERSION 1
+/* 2: LCML_FP8_DYNAMIC_WORKSPACE_BYTES grew from 256 to 4096 */
+#define LCML_FP8_ABI_VERSION 2
 
 /* status codes */
 #define LCML_OK 0
@@ -103,12 +104,13 @@ LCML_API int lcml_fp8_dequantize(const uint8_t *x, float *y, int64_t outer, int6
  * Dynamic per-tensor quantisation:  amax = max |x| over non-NaN elements,
  * scale = amax / 448 (1.0 when that is not a positive finite number),
  * y = from_float(x / scale).  Writes the scale to *scale_out (device).
- * workspace: device memory of LCML_FP8_DYNAMIC_WORKSPACE_BYTES; may be NULL
- * when n <= LCML_FP8_DYNAMIC_SMALL_MAX (one-workgroup path).
+ * workspace: device memory of LCML_FP8_DYNAMIC_WORKSPACE_BYTES (per-workgroup
+ * partial maxima, written before they are read: it needs no clearing); may
+ * be NULL when n <= LCML_FP8_DYNAMIC_SMALL_MAX (one-launch path).
  * The reference has no dynamic quantiser; its nearest composition would be
  * Abs -> ReduceMax (src/onnx/operators/reduce.cpp:417-459) -> Div -> Cast.
  */
-#define LCML_FP8_DYNAMIC_WORKSPACE_BYTES 256
+#define LCML_FP8_DYNAMIC_WORKSPACE_BYTES 4096
 #define LCML_FP8_DYNAMIC_SMALL_MAX 65536
 LCML_API int lcml_fp8_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
                               void *workspace, void *stream);

@@ -20,7 +20,7 @@ OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
 DTYPE_FLOAT, DTYPE_BFLOAT16, DTYPE_FLOAT8E4M3FN = 1, 16, 17
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_MFMA, KERNEL_SKINNY, KERNEL_VALU, KERNEL_MFMA_FP8, KERNEL_SKINNY_FP8 = 0, 1, 2, 3, 4, 5
-DYNAMIC_WORKSPACE_BYTES = 256
+DYNAMIC_WORKSPACE_BYTES = 4096
 DYNAMIC_SMALL_MAX = 65536
 PACK_K, PANEL_COLS = 128, 64
 

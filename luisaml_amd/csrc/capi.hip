@@ -199,12 +199,13 @@ bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kern
     return fits && (kernel == LCML_KERNEL_SKINNY || kernel == LCML_KERNEL_SKINNY_FP8);
 }
 int64_t pad256(int64_t n) { return (n + 255) / 256 * 256; }
+static_assert(LCML_FP8_DYNAMIC_WORKSPACE_BYTES >= lcml::kMaxAmaxPartials * 4, "workspace holds the partial maxima");
 }  // namespace
 
 int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel) {
     if (M <= 0 || K <= 0) return 0;
     if (dynamic_fusable(M, K, nullptr, K, kernel)) return 0;
-    // quantised activations, the amax word block, the scale (when not returned)
+    // quantised activations, the partial maxima, the scale (when not returned)
     return pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256;
 }
 
@@ -237,9 +238,9 @@ int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64
                     (long long)need);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     uint8_t *q = ws;
-    uint32_t *amax_word = reinterpret_cast<uint32_t *>(ws + pad256(M * K));
+    uint32_t *part = reinterpret_cast<uint32_t *>(ws + pad256(M * K));
     float *scale = x_scale_out ? x_scale_out : reinterpret_cast<float *>(ws + pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
-    hipError_t err = lcml::launch_quantize_dynamic(x, q, M * K, scale, amax_word, s);
+    hipError_t err = lcml::launch_quantize_dynamic(x, q, M * K, scale, part, s);
     if (err != hipSuccess) return hip_status(err, fn);
     return lcml_fp8_gemm(M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
                          c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
@@ -257,14 +258,15 @@ int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64_t c, int
     if (!aligned(y, 4)) return fail(LCML_ERR_INVALID_ARG, "%s: y must be 4-byte aligned", fn);
     hipStream_t s = (hipStream_t)stream;
     if (y_scale)
-        return hip_status(lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, y_scale, nullptr, nullptr, s),
+        return hip_status(lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, y_scale, nullptr, 0, nullptr, s),
                           fn);
     if (!scale_out || !workspace)
         return fail(LCML_ERR_INVALID_ARG, "%s: the dynamic scale needs scale_out and a workspace", fn);
-    uint32_t *word = static_cast<uint32_t *>(workspace);
-    hipError_t err = lcml::launch_fill_u32(word, 0u, 1, s);
-    if (err == hipSuccess) err = lcml::launch_amax(x, n * c * h * w, word, s);
-    if (err == hipSuccess) err = lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, nullptr, word, scale_out, s);
+    uint32_t *part = static_cast<uint32_t *>(workspace);
+    int npart = 0;
+    hipError_t err = lcml::launch_amax_partials(x, n * c * h * w, part, &npart, s);
+    if (err == hipSuccess)
+        err = lcml::launch_quantize_nhwc(x, y, n, (int)c, (int)h, (int)w, nullptr, part, npart, scale_out, s);
     return hip_status(err, fn);
 }
 

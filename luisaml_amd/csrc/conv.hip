@@ -1,8 +1,8 @@
 // conv.hip -- the data-layout kernels around the implicit-im2col FP8 conv:
 //   * QuantizeLinear of an NCHW fp32 activation straight into the NHWC E4M3
-//     layout the conv GEMM reads (per-tensor scale, static or from a reduced
-//     amax), through an LDS transpose so both the fp32 reads (along W) and
-//     the byte writes (along C) are contiguous;
+//     layout the conv GEMM reads (per-tensor scale, static or from partial
+//     maxima), through an LDS transpose so both the fp32 reads (along H*W)
+//     and the byte writes (along C) are contiguous and 16 bytes wide;
 //   * load-time packing of E4M3 conv weights [Cout][Cin][KH][KW] into the
 //     packed-panel GEMM layout with K ordered (kh, kw, c) and N = Cout.
 #include "lcml_internal.hpp"
@@ -10,43 +10,96 @@
 namespace lcml {
 namespace {
 
-constexpr int kTile = 64;  // 64 channels x 64 pixels of one image row per workgroup
+constexpr int kPix = 64;   // pixels of the flattened H*W plane per workgroup
+constexpr int kPQ = kPix / 4;  // pixel quads per tile
 constexpr int kThreads = 256;
 
-// grid: (Nb*H, ceil(W/64), ceil(C/64)); requires C % 4 == 0 (4-byte stores)
-template <bool FROM_AMAX>
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// NCHW fp32 -> NHWC E4M3: per image a [C][H*W] -> [H*W][C] transpose with the
+// quantiser in between.  Workgroup tile: kPix consecutive pixels x CT
+// channels.  Thread t owns pixel quad t % kPQ and channel quads
+// t / kPQ + (kThreads / kPQ) j: it reads four
+// channel rows x four pixels (one float4 per row when VEC, i.e. H*W % 4 == 0
+// and x 16-byte aligned), quantises them, and writes four 32-bit words (one
+// pixel's four channels each) into the LDS tile [pixel][channel]; the tile
+// then leaves as 16-byte pieces of each pixel's channel run (STORE16: C % 16
+// == 0 and y 16-byte aligned; else 32-bit stores, C % 4 == 0).  The x loads
+// are issued before the scale is known, so with a dynamic scale the
+// reduction of the partial maxima overlaps them.
+// grid: (Nb * ceil(HW/kPix), ceil(C/CT))
+template <int CT, bool FROM_AMAX, bool VEC, bool STORE16>
 __global__ __launch_bounds__(kThreads) void k_quantize_nchw_to_nhwc(const float *__restrict__ x,
-                                                                    uint8_t *__restrict__ y, int C, int H, int W,
-                                                                    const float *__restrict__ scale,
-                                                                    const uint32_t *__restrict__ amax_bits,
+                                                                    uint8_t *__restrict__ y, int C, int64_t HW,
+                                                                    int tiles_p, const float *__restrict__ scale,
+                                                                    const uint32_t *__restrict__ part, int npart,
                                                                     float *__restrict__ scale_out) {
-    __shared__ uint8_t tile[kTile][kTile + 4];  // [pixel][channel]
-    const int w0 = blockIdx.y * kTile, c0 = blockIdx.z * kTile;
-    const int n = blockIdx.x / H, h = blockIdx.x - n * H;
-    const float s = FROM_AMAX ? scale_from_amax_bits(*amax_bits) : scale[0];
-    if (FROM_AMAX && scale_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
-        *scale_out = s;
-    const Recip d = make_recip(s);
-    const int64_t plane = (int64_t)H * W;
-    // read: 64 channel rows x 64 pixels, contiguous along W
-    for (int idx = threadIdx.x; idx < kTile * kTile; idx += kThreads) {
-        const int c = idx / kTile, w = idx - c * kTile;
-        uint32_t code = 0;
-        if (c0 + c < C && w0 + w < W) {
-            const float v = x[((int64_t)n * C + c0 + c) * plane + (int64_t)h * W + w0 + w];
-            code = e4m3x2_hw(div_by(v, d), 0.0f) & 0xffu;
+    constexpr int CQP = kThreads / kPQ;  // channel quads per pass
+    constexpr int J = CT / 4 / CQP;      // passes
+    static_assert(J >= 1 && J * CQP * 4 == CT && (kPix * CT / 16) % kThreads == 0, "tile shape");
+    constexpr int PITCH = CT / 4 + 1;   // LDS words per pixel row (odd: writes spread over all banks)
+    __shared__ uint32_t tile[kPix * PITCH];
+    __shared__ float red[kThreads / 64];
+    const int n = blockIdx.x / tiles_p;
+    const int64_t p0 = (int64_t)(blockIdx.x - n * tiles_p) * kPix;
+    const int c0 = blockIdx.y * CT;
+    const int pq = threadIdx.x % kPQ;
+    const int64_t p = p0 + 4 * pq;
+    const float *xn = x + (int64_t)n * C * HW;
+    f4 v[J][4];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = c0 + 4 * (threadIdx.x / kPQ + CQP * j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[j][i] = f4{0.f, 0.f, 0.f, 0.f};
+            if (c < C) {  // C % 4 == 0: a channel quad is whole
+                const float *row = xn + (int64_t)(c + i) * HW + p;
+                if (VEC) {
+                    if (p < HW) v[j][i] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(row));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (p + e < HW) v[j][i][e] = row[e];
+                }
+            }
         }
-        tile[w][c] = (uint8_t)code;
+    }
+    float s;
+    if (FROM_AMAX) {
+        s = scale_from_partials<kThreads>(part, npart, red);
+        if (scale_out && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *scale_out = s;
+    } else {
+        s = scale[0];
+    }
+    const Recip d = make_recip(s);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int cq = threadIdx.x / kPQ + CQP * j;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            tile[(4 * pq + e) * PITCH + cq] = quantize4(v[j][0][e], v[j][1][e], v[j][2][e], v[j][3][e], d);
     }
     __syncthreads();
-    // write: per pixel 64 contiguous channel bytes, 4 per thread
-    uint8_t *yrow = y + (((int64_t)n * H + h) * W) * C;
-    for (int idx = threadIdx.x; idx < kTile * (kTile / 4); idx += kThreads) {
-        const int w = idx / (kTile / 4), c4 = (idx - w * (kTile / 4)) * 4;
-        if (w0 + w < W && c0 + c4 < C) {
-            const uint32_t v = (uint32_t)tile[w][c4] | ((uint32_t)tile[w][c4 + 1] << 8) |
-                               ((uint32_t)tile[w][c4 + 2] << 16) | ((uint32_t)tile[w][c4 + 3] << 24);
-            *reinterpret_cast<uint32_t *>(yrow + (int64_t)(w0 + w) * C + c0 + c4) = v;
+    constexpr int CHUNKS = CT / 16;  // 16-byte pieces per pixel
+    uint8_t *yn = y + (int64_t)n * HW * C;
+#pragma unroll
+    for (int k0 = 0; k0 < kPix * CHUNKS; k0 += kThreads) {
+        const int k = k0 + threadIdx.x;
+        const int pp = k / CHUNKS, ch = k - pp * CHUNKS;
+        const int64_t pix = p0 + pp;
+        const int cc = c0 + 16 * ch;
+        if (pix >= HW || cc >= C) continue;
+        const uint32_t *src = &tile[pp * PITCH + 4 * ch];
+        uint8_t *dst = yn + pix * C + cc;
+        if (STORE16) {
+            const u4 w = {src[0], src[1], src[2], src[3]};
+            *reinterpret_cast<u4 *>(dst) = w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (cc + 4 * q < C) reinterpret_cast<uint32_t *>(dst)[q] = src[q];
         }
     }
 }
@@ -80,17 +133,42 @@ __global__ void k_pack_conv_weight(const uint8_t *__restrict__ w, int Mg, int Ci
     dst[0] = out[0]; dst[1] = out[1]; dst[2] = out[2]; dst[3] = out[3];
 }
 
+template <int CT, bool FROM_AMAX>
+void launch_nhwc_ct(const float *x, uint8_t *y, int64_t Nb, int C, int64_t HW, bool vec, bool store16,
+                    const float *scale, const uint32_t *part, int npart, float *scale_out, hipStream_t s) {
+    const int tiles_p = (int)((HW + kPix - 1) / kPix);
+    dim3 grid((unsigned)(Nb * tiles_p), (unsigned)((C + CT - 1) / CT));
+#define LCML_NHWC(V, S)                                                                                          \
+    hipLaunchKernelGGL((k_quantize_nchw_to_nhwc<CT, FROM_AMAX, V, S>), grid, dim3(kThreads), 0, s, x, y, C, HW, \
+                       tiles_p, scale, part, npart, scale_out)
+    if (vec) {
+        if (store16) LCML_NHWC(true, true); else LCML_NHWC(true, false);
+    } else {
+        if (store16) LCML_NHWC(false, true); else LCML_NHWC(false, false);
+    }
+#undef LCML_NHWC
+}
+
+template <bool FROM_AMAX>
+void launch_nhwc(const float *x, uint8_t *y, int64_t Nb, int C, int64_t HW, const float *scale, const uint32_t *part,
+                 int npart, float *scale_out, hipStream_t s) {
+    const bool vec = HW % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool store16 = C % 16 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    if (C % 128 == 0)
+        launch_nhwc_ct<128, FROM_AMAX>(x, y, Nb, C, HW, vec, store16, scale, part, npart, scale_out, s);
+    else
+        launch_nhwc_ct<64, FROM_AMAX>(x, y, Nb, C, HW, vec, store16, scale, part, npart, scale_out, s);
+}
+
 }  // namespace
 
 hipError_t launch_quantize_nhwc(const float *x, uint8_t *y, int64_t Nb, int C, int H, int W, const float *scale,
-                                const uint32_t *amax_bits, float *scale_out, hipStream_t s) {
-    dim3 grid((unsigned)(Nb * H), (unsigned)((W + kTile - 1) / kTile), (unsigned)((C + kTile - 1) / kTile));
-    if (amax_bits)
-        hipLaunchKernelGGL(k_quantize_nchw_to_nhwc<true>, grid, dim3(kThreads), 0, s, x, y, C, H, W, scale,
-                           amax_bits, scale_out);
+                                const uint32_t *part, int npart, float *scale_out, hipStream_t s) {
+    const int64_t HW = (int64_t)H * W;
+    if (part)
+        launch_nhwc<true>(x, y, Nb, C, HW, scale, part, npart, scale_out, s);
     else
-        hipLaunchKernelGGL(k_quantize_nchw_to_nhwc<false>, grid, dim3(kThreads), 0, s, x, y, C, H, W, scale,
-                           amax_bits, scale_out);
+        launch_nhwc<false>(x, y, Nb, C, HW, scale, nullptr, 0, nullptr, s);
     return hipGetLastError();
 }
 

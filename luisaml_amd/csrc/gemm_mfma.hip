@@ -410,12 +410,24 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             if (col < e.N) {
                 const float sc = epi_scale(e, a_s, col);
                 const int64_t row0 = m0 + wm * WM * 32 + (lane >> 5);
+                if (!e.c || epi_c_row_invariant(e)) {
+                    // scale and bias per column, read once; rows unrolled so
+                    // several stores are in flight
+                    const float cv = e.c ? epi_c(e, 0, col) : 0.0f;
+#pragma unroll 4
+                    for (int q = 0; q < WM * 16; ++q) {
+                        const int64_t row = row0 + 2 * q;
+                        const float v = epi_value_cv(e, sc, cv, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]);
+                        if (row < e.M) epi_store(e, row, col, v);
+                    }
+                } else {
 #pragma unroll 1
-                for (int q = 0; q < WM * 16; ++q) {
-                    const int64_t row = row0 + 2 * q;
-                    if (row >= e.M) break;
-                    epi_store(e, row, col,
-                              epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
+                    for (int q = 0; q < WM * 16; ++q) {
+                        const int64_t row = row0 + 2 * q;
+                        if (row >= e.M) break;
+                        epi_store(e, row, col,
+                                  epi_value(e, sc, row, col, st[(2 * q + (lane >> 5)) * EP_PITCH + (lane & 31)]));
+                    }
                 }
             }
         }

@@ -105,6 +105,45 @@ __device__ inline float scale_from_amax_bits(uint32_t bits) {
     return s;
 }
 
+// max over a wavefront / a workgroup of THREADS threads (red: THREADS/64
+// floats of LDS); every thread gets the result
+__device__ inline float wave_max(float m) {
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+
+template <int THREADS>
+__device__ inline float block_max(float m, float *red) {
+    m = wave_max(m);
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (wave == 0) {
+        m = lane < THREADS / 64 ? red[lane] : 0.0f;
+        m = wave_max(m);
+        if (lane == 0) red[0] = m;
+    }
+    __syncthreads();
+    m = red[0];
+    __syncthreads();
+    return m;
+}
+
+// the dynamic scale from npart partial maxima (fp32 bits of non-negative
+// floats, one per workgroup of the amax pass); called by whole workgroups
+template <int THREADS>
+__device__ inline float scale_from_partials(const uint32_t *part, int npart, float *red) {
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < npart; i += THREADS) {
+        const float v = bits_f32(part[i]);
+        m = v > m ? v : m;
+    }
+    return scale_from_amax_bits(f32_bits(block_max<THREADS>(m, red)));
+}
+
 // four consecutive elements quantised with one scale -> four packed codes
 __device__ inline uint32_t quantize4(float a, float b, float c, float e, const Recip &d) {
     return e4m3x2_hw(div_by(a, d), div_by(b, d)) | (e4m3x2_hw(div_by(c, d), div_by(e, d)) << 16);
@@ -120,12 +159,15 @@ __host__ __device__ inline uint16_t bf16_rne(float f) {
 
 // Abramowitz & Stegun 7.1.26 erf, as in the reference
 // (include/onnx/operators/common.h:176-195).
+// The reciprocal and the exponential use the hardware approximations
+// (v_rcp_f32, v_exp_f32; a few ulp), which keeps GELU epilogues cheap; the
+// formula's own error (|err| <= 1.5e-7) is of the same order.
 __device__ inline float as_erf(float x) {
     float ax = fabsf(x);
-    float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * ax);
     float poly = t * (0.254829592f +
                       t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
-    float r = 1.0f - poly * expf(-ax * ax);
+    float r = 1.0f - poly * __expf(-ax * ax);
     return x < 0.0f ? -r : r;
 }
 
@@ -172,6 +214,22 @@ __device__ inline float epi_value(const Epilogue &e, float scale_n, int64_t m, i
     float v = acc * scale_n;
     if (e.alpha != 1.0f) v *= e.alpha;
     if (e.c) v = e.beta == 1.0f ? v + epi_c(e, m, n) : v + e.beta * epi_c(e, m, n);
+    return apply_act(v, e.act);
+}
+
+// True when C's broadcast value does not depend on the row m (a bias over
+// N, or a scalar), so an epilogue with a fixed column per lane reads it once.
+__device__ inline bool epi_c_row_invariant(const Epilogue &e) {
+    if (e.c_ndim == 0 || (e.c_ndim == 1 && (e.c0 == 1 || e.c0 == e.N))) return true;
+    return e.c_ndim == 2 && e.c0 == 1;
+}
+
+// epi_value with C's element already read (cv; ignored without C): the same
+// operations in the same order
+__device__ inline float epi_value_cv(const Epilogue &e, float scale_n, float cv, float acc) {
+    float v = acc * scale_n;
+    if (e.alpha != 1.0f) v *= e.alpha;
+    if (e.c) v = e.beta == 1.0f ? v + cv : v + e.beta * cv;
     return apply_act(v, e.act);
 }
 

@@ -15,6 +15,9 @@ hipError_t launch_dequantize(const uint8_t *x, float *y, int64_t outer, int64_t 
                              int64_t inner, const float *scale, hipStream_t s);
 // amax into a zero-initialised uint word (atomic max on fp32 bits)
 hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream_t s);
+// partial maxima (at most kMaxAmaxPartials words at part); *npart = count
+constexpr int kMaxAmaxPartials = 1024;
+hipError_t launch_amax_partials(const float *x, int64_t n, uint32_t *part, int *npart, hipStream_t s);
 hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
                                    uint32_t *work, hipStream_t s);
 hipError_t launch_amax_to_float(const uint32_t *amax_bits, float *out, hipStream_t s);
@@ -37,9 +40,10 @@ hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int
                             int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int group, int OH, int OW,
                             const Epilogue &e, bool exact, hipStream_t s);
 // NCHW fp32 -> NHWC E4M3 with a per-tensor scale: scale[0], or amax/448 from
-// *amax_bits when amax_bits is given (then written to scale_out if non-null)
+// npart partial maxima when part is given (then written to scale_out if
+// non-null)
 hipError_t launch_quantize_nhwc(const float *x, uint8_t *y, int64_t Nb, int C, int H, int W, const float *scale,
-                                const uint32_t *amax_bits, float *scale_out, hipStream_t s);
+                                const uint32_t *part, int npart, float *scale_out, hipStream_t s);
 // per group g: the packed GEMM weight of W[g*Cout/group ..][Cin_g][KH][KW],
 // blocks of packed_weight_bytes(KH*KW*Cin_g, Cout/group) one after another
 hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin_g, int KH, int KW, int group, uint8_t *packed,

@@ -1,17 +1,16 @@
 // quantize.hip -- QuantizeLinear / DequantizeLinear / amax kernels (gfx950).
 //
 // All three are HBM-bound streaming kernels (4 B in + 1 B out per element
-// for quantize, 1 B in + 4 B out for dequantize).  Each thread moves 16
-// elements: four 128-bit fp32 loads and one 128-bit fp8 store (or the
-// reverse), so every wavefront instruction touches 1 KB (fp8 side) or 4 KB
-// (fp32 side) of contiguous memory.
+// for quantize, 1 B in + 4 B out for dequantize).  The vector paths move one
+// float4 <-> one 32-bit code word per lane per instruction, so a wavefront
+// instruction touches 1 KB (fp32 side) or 256 B (fp8 side) of contiguous
+// memory, with eight such float4s per thread in flight.
 #include "lcml_internal.hpp"
 
 namespace lcml {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kVec = 16;  // elements per thread per step
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
@@ -22,27 +21,59 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 __device__ inline uint32_t enc4(f4 v, const Recip &d) { return quantize4(v.x, v.y, v.z, v.w, d); }
 
 
-// Per-tensor (or per-axis with a 16-element-uniform scale index) vector path.
-// grid-stride over 16-element groups; requires x, y 16-byte aligned.
+// Vector path, per-tensor or per-axis with inner % 4 == 0 (one scale per
+// float4); requires x 16-byte and y 4-byte aligned.  Each thread encodes kU
+// float4s per pass, taken kThreads apart so that every load instruction of a
+// wavefront reads 1 KB and every store writes 256 contiguous bytes (kU = 4
+// measured a little faster than 8 or 16 on 16M-45M element tensors).  The first pass's loads are issued before
+// the scale is known (with a dynamic scale, its reduction from the partial
+// maxima overlaps them) and each later pass's before the previous pass's
+// stores.
+constexpr int kU = 4;
+
 template <bool FROM_AMAX>
 __global__ __launch_bounds__(kThreads) void k_quantize_vec(const float *__restrict__ x,
-                                                           uint8_t *__restrict__ y, int64_t ngroups,
+                                                           uint8_t *__restrict__ y, int64_t n4,
                                                            int64_t axis_len, int64_t inner,
                                                            const float *__restrict__ scale,
-                                                           const uint32_t *__restrict__ amax_bits) {
+                                                           const uint32_t *__restrict__ part, int npart,
+                                                           float *__restrict__ scale_out) {
+    __shared__ float red[kThreads / 64];
+    const f4 *x4 = reinterpret_cast<const f4 *>(x);
+    uint32_t *y4 = reinterpret_cast<uint32_t *>(y);
+    const int64_t stride = (int64_t)gridDim.x * kThreads * kU;
+    int64_t i0 = (int64_t)blockIdx.x * kThreads * kU + threadIdx.x;
+    f4 v[kU];
+    auto load = [&](int64_t b) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t i = b + (int64_t)u * kThreads;
+            v[u] = i < n4 ? __builtin_nontemporal_load(x4 + i) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    load(i0);
     float s_tensor = 1.0f;
-    if (FROM_AMAX) s_tensor = scale_from_amax_bits(*amax_bits);
-    else if (axis_len == 1) s_tensor = scale[0];
+    if (FROM_AMAX) {
+        s_tensor = scale_from_partials<kThreads>(part, npart, red);
+        if (scale_out && blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s_tensor;
+    } else if (axis_len == 1) {
+        s_tensor = scale[0];
+    }
     const Recip d_tensor = make_recip(s_tensor);
-    int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x; g < ngroups; g += stride) {
-        // per-axis: one scale per 16-element group (inner % 16 == 0)
-        const Recip d = (!FROM_AMAX && axis_len != 1) ? make_recip(scale[((g * kVec) / inner) % axis_len]) : d_tensor;
-        const f4 *xp = reinterpret_cast<const f4 *>(x + g * kVec);
-        f4 v0 = __builtin_nontemporal_load(xp + 0), v1 = __builtin_nontemporal_load(xp + 1);
-        f4 v2 = __builtin_nontemporal_load(xp + 2), v3 = __builtin_nontemporal_load(xp + 3);
-        u4 out = {enc4(v0, d), enc4(v1, d), enc4(v2, d), enc4(v3, d)};
-        *reinterpret_cast<u4 *>(y + g * kVec) = out;
+    for (; i0 < n4; i0 += stride) {
+        uint32_t code[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t i = i0 + (int64_t)u * kThreads;
+            const Recip d = (!FROM_AMAX && axis_len != 1) ? make_recip(scale[((i * 4) / inner) % axis_len]) : d_tensor;
+            code[u] = enc4(v[u], d);
+        }
+        if (i0 + stride < n4) load(i0 + stride);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t i = i0 + (int64_t)u * kThreads;
+            if (i < n4) y4[i] = code[u];
+        }
     }
 }
 
@@ -52,9 +83,12 @@ __global__ __launch_bounds__(kThreads) void k_quantize_scalar(const float *__res
                                                               uint8_t *__restrict__ y, int64_t begin,
                                                               int64_t n, int64_t axis_len, int64_t inner,
                                                               const float *__restrict__ scale,
-                                                              const uint32_t *__restrict__ amax_bits) {
+                                                              const uint32_t *__restrict__ part, int npart,
+                                                              float *__restrict__ scale_out) {
+    __shared__ float red[kThreads / 64];
     int64_t stride = (int64_t)gridDim.x * kThreads;
-    float s_amax = FROM_AMAX ? scale_from_amax_bits(*amax_bits) : 0.0f;
+    float s_amax = FROM_AMAX ? scale_from_partials<kThreads>(part, npart, red) : 0.0f;
+    if (FROM_AMAX && scale_out && blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s_amax;
     for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
         float s = FROM_AMAX ? s_amax : scale[axis_len == 1 ? 0 : (i / inner) % axis_len];
         y[i] = (uint8_t)e4m3_encode(__fdiv_rn(x[i], s));
@@ -70,19 +104,34 @@ __device__ inline void dec4(uint32_t w, float s, f4 &o) {
     o.x = lo.x * s; o.y = lo.y * s; o.z = hi.x * s; o.w = hi.y * s;
 }
 
+// Same shape as k_quantize_vec with kUd 32-bit code words per thread,
+// kThreads apart; requires q 4-byte and y 16-byte aligned, inner % 4 == 0
+// per axis.
+constexpr int kUd = 8;
+
 __global__ __launch_bounds__(kThreads) void k_dequantize_vec(const uint8_t *__restrict__ q,
-                                                             float *__restrict__ y, int64_t ngroups,
+                                                             float *__restrict__ y, int64_t n4,
                                                              int64_t axis_len, int64_t inner,
                                                              const float *__restrict__ scale) {
-    float s_tensor = axis_len == 1 ? scale[0] : 0.0f;
-    int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x; g < ngroups; g += stride) {
-        float s = axis_len == 1 ? s_tensor : scale[((g * kVec) / inner) % axis_len];
-        u4 w = __builtin_nontemporal_load(reinterpret_cast<const u4 *>(q + g * kVec));
-        f4 o0, o1, o2, o3;
-        dec4(w.x, s, o0); dec4(w.y, s, o1); dec4(w.z, s, o2); dec4(w.w, s, o3);
-        f4 *yp = reinterpret_cast<f4 *>(y + g * kVec);
-        yp[0] = o0; yp[1] = o1; yp[2] = o2; yp[3] = o3;
+    const uint32_t *q4 = reinterpret_cast<const uint32_t *>(q);
+    f4 *y4 = reinterpret_cast<f4 *>(y);
+    const float s_tensor = axis_len == 1 ? scale[0] : 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads * kUd;
+    for (int64_t i0 = (int64_t)blockIdx.x * kThreads * kUd + threadIdx.x; i0 < n4; i0 += stride) {
+        uint32_t w[kUd];
+#pragma unroll
+        for (int u = 0; u < kUd; ++u) {
+            const int64_t i = i0 + (int64_t)u * kThreads;
+            w[u] = i < n4 ? __builtin_nontemporal_load(q4 + i) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kUd; ++u) {
+            const int64_t i = i0 + (int64_t)u * kThreads;
+            const float sc = axis_len == 1 ? s_tensor : scale[((i * 4) / inner) % axis_len];
+            f4 o;
+            dec4(w[u], sc, o);
+            if (i < n4) y4[i] = o;
+        }
     }
 }
 
@@ -104,41 +153,12 @@ __device__ inline float absmax_acc(float m, float v) {
     return a > m ? a : m;  // NaN compares false and is skipped
 }
 
-__device__ inline float wave_max(float m) {
-    for (int off = 32; off > 0; off >>= 1) {
-        float o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    return m;
-}
-
-template <int THREADS>
-__device__ inline float block_max(float m, float *red) {
-    m = wave_max(m);
-    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    if (wave == 0) {
-        m = lane < THREADS / 64 ? red[lane] : 0.0f;
-        m = wave_max(m);
-        if (lane == 0) red[0] = m;
-    }
-    __syncthreads();
-    m = red[0];
-    __syncthreads();
-    return m;
-}
-
-// amax: each block reduces its grid-stride share (8 float4 loads in flight
-// per thread), then one atomic max on the fp32 bits (non-negative floats
-// order like their unsigned bit patterns).  The grid is capped at 256
-// workgroups so the same-address atomics stay few.
 constexpr int kAmaxThreads = 512;
 constexpr int kAmaxU = 8;
 
-__global__ __launch_bounds__(kAmaxThreads) void k_amax(const float *__restrict__ x, int64_t n,
-                                                       uint32_t *__restrict__ amax_bits) {
-    __shared__ float red[kAmaxThreads / 64];
+// this workgroup's max |x| over its grid-stride share (8 float4 loads in
+// flight per thread); every thread gets the result
+__device__ inline float wg_amax(const float *__restrict__ x, int64_t n, float *red) {
     float m = 0.0f;
     bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
     const int64_t nv = vec ? n / 4 : 0;
@@ -160,17 +180,33 @@ __global__ __launch_bounds__(kAmaxThreads) void k_amax(const float *__restrict__
     for (int64_t i = nv * 4 + (int64_t)blockIdx.x * kAmaxThreads + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kAmaxThreads)
         m = absmax_acc(m, x[i]);
-    m = block_max<kAmaxThreads>(m, red);
+    return block_max<kAmaxThreads>(m, red);
+}
+
+// amax into one word: one atomic max per workgroup on the fp32 bits
+// (non-negative floats order like their unsigned bit patterns); the grid is
+// capped at 256 workgroups so the same-address atomics stay few.
+__global__ __launch_bounds__(kAmaxThreads) void k_amax(const float *__restrict__ x, int64_t n,
+                                                       uint32_t *__restrict__ amax_bits) {
+    __shared__ float red[kAmaxThreads / 64];
+    const float m = wg_amax(x, n, red);
     if (threadIdx.x == 0) atomicMax(amax_bits, f32_bits(m));
+}
+
+// Partial maxima: workgroup b stores its maximum (fp32 bits) in part[b].
+// Every entry is written, so the buffer needs no clearing and no atomics are
+// involved; the consumer reduces the gridDim.x entries itself
+// (scale_from_partials).
+__global__ __launch_bounds__(kAmaxThreads) void k_amax_partials(const float *__restrict__ x, int64_t n,
+                                                                uint32_t *__restrict__ part) {
+    __shared__ float red[kAmaxThreads / 64];
+    const float m = wg_amax(x, n, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = f32_bits(m);
 }
 
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
-}
-
-__global__ void k_amax_finalize(const uint32_t *amax_bits, float *scale_out) {
-    if (threadIdx.x == 0) *scale_out = scale_from_amax_bits(*amax_bits);
 }
 
 __global__ void k_amax_to_float(const uint32_t *amax_bits, float *out) {
@@ -240,7 +276,15 @@ int grid_for(int64_t work_items, int64_t cap = 4096) {
     return (int)g;
 }
 
+// workgroups for the vector kernels: u float4 / code words per thread per
+// pass, at most 4096 workgroups (grid-stride beyond)
+int grid_vec(int64_t n4, int u) {
+    int64_t g = (n4 + (int64_t)kThreads * u - 1) / ((int64_t)kThreads * u);
+    return (int)(g < 1 ? 1 : (g > 4096 ? 4096 : g));
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; }
 
 }  // namespace
 
@@ -248,14 +292,14 @@ hipError_t launch_quantize(const float *x, uint8_t *y, int64_t outer, int64_t ax
                            int64_t inner, const float *scale, hipStream_t s) {
     int64_t n = outer * axis_len * inner;
     if (n == 0) return hipSuccess;
-    bool group_uniform = axis_len == 1 || inner % kVec == 0;
-    int64_t ngroups = (aligned16(x) && aligned16(y) && group_uniform) ? n / kVec : 0;
-    if (ngroups)
-        hipLaunchKernelGGL(k_quantize_vec<false>, dim3(grid_for(ngroups)), dim3(kThreads), 0, s, x, y,
-                           ngroups, axis_len, inner, scale, nullptr);
-    if (ngroups * kVec < n)
-        hipLaunchKernelGGL(k_quantize_scalar<false>, dim3(grid_for(n - ngroups * kVec)), dim3(kThreads),
-                           0, s, x, y, ngroups * kVec, n, axis_len, inner, scale, nullptr);
+    const bool quad_uniform = axis_len == 1 || inner % 4 == 0;
+    const int64_t n4 = (aligned16(x) && aligned4(y) && quad_uniform) ? n / 4 : 0;
+    if (n4)
+        hipLaunchKernelGGL(k_quantize_vec<false>, dim3(grid_vec(n4, kU)), dim3(kThreads), 0, s, x, y, n4, axis_len,
+                           inner, scale, nullptr, 0, nullptr);
+    if (n4 * 4 < n)
+        hipLaunchKernelGGL(k_quantize_scalar<false>, dim3(grid_for(n - n4 * 4)), dim3(kThreads), 0, s, x, y,
+                           n4 * 4, n, axis_len, inner, scale, nullptr, 0, nullptr);
     return hipGetLastError();
 }
 
@@ -263,14 +307,14 @@ hipError_t launch_dequantize(const uint8_t *x, float *y, int64_t outer, int64_t 
                              int64_t inner, const float *scale, hipStream_t s) {
     int64_t n = outer * axis_len * inner;
     if (n == 0) return hipSuccess;
-    bool group_uniform = axis_len == 1 || inner % kVec == 0;
-    int64_t ngroups = (aligned16(x) && aligned16(y) && group_uniform) ? n / kVec : 0;
-    if (ngroups)
-        hipLaunchKernelGGL(k_dequantize_vec, dim3(grid_for(ngroups)), dim3(kThreads), 0, s, x, y,
-                           ngroups, axis_len, inner, scale);
-    if (ngroups * kVec < n)
-        hipLaunchKernelGGL(k_dequantize_scalar, dim3(grid_for(n - ngroups * kVec)), dim3(kThreads), 0,
-                           s, x, y, ngroups * kVec, n, axis_len, inner, scale);
+    const bool quad_uniform = axis_len == 1 || inner % 4 == 0;
+    const int64_t n4 = (aligned4(x) && aligned16(y) && quad_uniform) ? n / 4 : 0;
+    if (n4)
+        hipLaunchKernelGGL(k_dequantize_vec, dim3(grid_vec(n4, kUd)), dim3(kThreads), 0, s, x, y, n4, axis_len, inner,
+                           scale);
+    if (n4 * 4 < n)
+        hipLaunchKernelGGL(k_dequantize_scalar, dim3(grid_for(n - n4 * 4)), dim3(kThreads), 0, s, x, y, n4 * 4, n,
+                           axis_len, inner, scale);
     return hipGetLastError();
 }
 
@@ -286,15 +330,26 @@ hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream
     return hipGetLastError();
 }
 
+hipError_t launch_amax_partials(const float *x, int64_t n, uint32_t *part, int *npart, hipStream_t s) {
+    // one workgroup per CU at most (grid-stride beyond), which measured
+    // faster than 512 or 1024 workgroups on 16M-45M element tensors
+    constexpr int64_t kGrid = 256;
+    static_assert(kGrid <= kMaxAmaxPartials, "partials fit the workspace");
+    int64_t g = (n / 4 + (int64_t)kAmaxThreads * kAmaxU - 1) / ((int64_t)kAmaxThreads * kAmaxU);
+    g = g < 1 ? 1 : (g > kGrid ? kGrid : g);
+    *npart = (int)g;
+    hipLaunchKernelGGL(k_amax_partials, dim3((unsigned)g), dim3(kAmaxThreads), 0, s, x, n, part);
+    return hipGetLastError();
+}
+
 hipError_t launch_amax_to_float(const uint32_t *amax_bits, float *out, hipStream_t s) {
     hipLaunchKernelGGL(k_amax_to_float, dim3(1), dim3(64), 0, s, amax_bits, out);
     return hipGetLastError();
 }
 
 // Dynamic per-tensor quantisation.  Small tensors: one workgroup, one launch.
-// Larger: zero the amax word, reduce, encode, then write the scale; `work`
-// is one device uint32 of scratch (the caller's scale_out is not reused for
-// it because the encode kernel reads the amax while running).
+// Larger: partial maxima into `work` (kMaxAmaxPartials words), then the
+// encode, whose every workgroup reduces them to the scale.
 hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
                                    uint32_t *work, hipStream_t s) {
     if (n <= kSmallMax) {
@@ -309,18 +364,18 @@ hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float 
                                scale_out);
         return hipGetLastError();
     }
-    hipError_t err = launch_fill_u32(work, 0u, 1, s);
+    // two launches: partial maxima into `work`, then the encode kernel(s),
+    // each workgroup of which reduces the partials to the scale
+    int npart = 0;
+    hipError_t err = launch_amax_partials(x, n, work, &npart, s);
     if (err != hipSuccess) return err;
-    err = launch_amax(x, n, work, s);
-    if (err != hipSuccess) return err;
-    int64_t ngroups = (aligned16(x) && aligned16(y)) ? n / kVec : 0;
-    if (ngroups)
-        hipLaunchKernelGGL(k_quantize_vec<true>, dim3(grid_for(ngroups)), dim3(kThreads), 0, s, x, y,
-                           ngroups, (int64_t)1, n, nullptr, work);
-    if (ngroups * kVec < n)
-        hipLaunchKernelGGL(k_quantize_scalar<true>, dim3(grid_for(n - ngroups * kVec)), dim3(kThreads),
-                           0, s, x, y, ngroups * kVec, n, (int64_t)1, n, nullptr, work);
-    hipLaunchKernelGGL(k_amax_finalize, dim3(1), dim3(64), 0, s, work, scale_out);
+    const int64_t n4 = (aligned16(x) && aligned4(y)) ? n / 4 : 0;
+    if (n4)
+        hipLaunchKernelGGL(k_quantize_vec<true>, dim3(grid_vec(n4, kU)), dim3(kThreads), 0, s, x, y, n4, (int64_t)1,
+                           n, nullptr, work, npart, scale_out);
+    if (n4 * 4 < n)
+        hipLaunchKernelGGL(k_quantize_scalar<true>, dim3(grid_for(n - n4 * 4)), dim3(kThreads), 0, s, x, y,
+                           n4 * 4, n, (int64_t)1, n, nullptr, work, npart, n4 ? nullptr : scale_out);
     return hipGetLastError();
 }
 

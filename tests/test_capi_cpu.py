@@ -23,8 +23,18 @@ def test_library_exports_every_declared_symbol():
         sorted(s for s in exported if not s.startswith("lcml_fp8_"))[:10]
 
 
+def header_define(name):
+    import re
+    m = re.search(r"#define\s+" + name + r"\s+(\d+)", open(capi.HEADER).read())
+    return int(m.group(1))
+
+
 def test_abi_version():
-    assert capi.lib().lcml_fp8_abi_version() == 1
+    assert capi.lib().lcml_fp8_abi_version() == header_define("LCML_FP8_ABI_VERSION") == 2
+
+
+def test_python_constants_match_header():
+    assert capi.DYNAMIC_WORKSPACE_BYTES == header_define("LCML_FP8_DYNAMIC_WORKSPACE_BYTES")
 
 
 def test_packed_weight_bytes():
