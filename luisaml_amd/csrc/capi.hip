@@ -178,6 +178,9 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     case LCML_KERNEL_SKINNY:
     case LCML_KERNEL_SKINNY_FP8:
         if (M > 16) return fail(LCML_ERR_UNSUPPORTED, "%s: the skinny kernel takes M <= 16 (M=%lld)", fn, (long long)M);
+        // buffer extents are 32-bit: the activations and one weight panel
+        if ((M - 1) * lda + K >= (int64_t)0x80000000 || lcml::pad_to(K, lcml::kPackK) * 64 >= (int64_t)0x80000000)
+            return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the skinny kernel", fn);
         err = lcml::launch_gemm_skinny(M, N, K, a, lda, b_packed, e, kernel == LCML_KERNEL_SKINNY, s);
         break;
     case LCML_KERNEL_VALU: err = lcml::launch_gemv_valu_fp8(M, N, K, a, lda, b_packed, e, s); break;
@@ -194,7 +197,7 @@ namespace {
 constexpr int64_t kAutoFuseMaxElems = 8192;
 bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kernel) {
     const bool fits = M <= 16 && lcml::skinny_dynamic_lds_bytes(M, K) <= lcml::kSkinnyDynLdsMax &&
-                      (!x || aligned(x, 16)) && ldx % 4 == 0;
+                      (!x || aligned(x, 16)) && ldx % 4 == 0 && ((M - 1) * ldx + K) * 4 < (int64_t)0x80000000;
     if (kernel == LCML_KERNEL_AUTO) return fits && M * K <= kAutoFuseMaxElems;
     return fits && (kernel == LCML_KERNEL_SKINNY || kernel == LCML_KERNEL_SKINNY_FP8);
 }

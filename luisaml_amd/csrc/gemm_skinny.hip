@@ -27,9 +27,10 @@
 // the 16 rows of a fragment read fall in distinct banks; k >= K is zero).
 // The main loop then reads the activation operand from LDS.  The redundant
 // per-workgroup amax and encode cost M*K loads and ~20 VALU operations per
-// element in every workgroup (measured on the 4096x11008 linear: +2.7 us at
-// M=1, +6 us at M=4 over the GEMM alone, against +4.5 us for the separate
-// quantise launch), so the fused kernel only pays off for small M*K.
+// element in every workgroup (measured on the 4096x11008 linear: +2.2 us at
+// M=1, +2.8 us at M=2, +5 us at M=4 over the GEMM alone, against about
+// +4.5 us for the separate quantise launch), so the fused kernel only pays
+// off for small M*K.
 #include "lcml_internal.hpp"
 
 namespace lcml {
@@ -44,6 +45,13 @@ namespace {
 #ifndef LCML_SKINNY_UNROLL
 #define LCML_SKINNY_UNROLL 1
 #endif
+#ifndef LCML_SKINNY_PF
+#define LCML_SKINNY_PF 2
+#endif
+
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every extent: loads return zeros
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer resource word 3 (as the tiled GEMM uses)
+constexpr int kNT = 2;                  // buffer load cache policy: non-temporal (streamed weights)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -77,36 +85,44 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     constexpr int NT = WAVES * 64;
     __shared__ v4f red[WAVES][NB][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // DYN: [M][pitch] E4M3
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wavefront index is uniform: readfirstlane lets the compiler keep
+    // everything derived from it (the K range, the in-range tests) scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t blk0 = (int64_t)blockIdx.x * NB;  // first 16-column block
 
     // K range of this wavefront
     const int kb_begin = (int)(((int64_t)g.nkb * wave) / WAVES);
     const int kb_end = (int)(((int64_t)g.nkb * (wave + 1)) / WAVES);
 
-    // activation operand: row lane%16, k offset (lane/16)*32 within a K block
+    // Every global load below is a buffer load whose out-of-range lanes and
+    // blocks carry an offset past the buffer's extent: the hardware returns
+    // zeros for them without touching memory.  So no load sits under a
+    // branch, the code from a load to its first use is straight-line, and the
+    // compiler's vmcnt waits count exactly the loads issued after it (a load
+    // under a branch makes it wait for every outstanding load instead, which
+    // would drain the weight prefetch at each use).
     const int arow = lane & 15;
     const bool a_ok = arow < g.M;
-    const uint8_t *a_ptr = g.a + (a_ok ? arow : 0) * g.lda + (lane >> 4) * 32;
 
-    // weight operand addresses for each 16-column block
-    const uint8_t *b_ptr[NB];
-    bool b_ok[NB];
+    // weights: this workgroup's 64-column panel (NB 16-column blocks)
+    const int64_t panel0 = blk0 >> 2;
+    const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g.bp + (panel0 < (g.nblk16 >> 2) ? panel0 : 0) * g.KC * 1024), 0, (int)(g.KC * 1024), kRsrcFlags);
+    uint32_t b_off[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        int64_t blk = blk0 + j;
-        b_ok[j] = blk < g.nblk16;
-        int64_t panel = (b_ok[j] ? blk : 0) >> 2, sub = blk & 3;
-        b_ptr[j] = g.bp + panel * g.KC * 1024 + (sub * 16 + (lane & 15)) * 16 +
-                   (int64_t)((lane >> 4) * 2) * 1024;
+        const int64_t blk = blk0 + j;
+        b_off[j] = blk < g.nblk16 ? (uint32_t)((((blk & 3) * 16 + (lane & 15)) * 16) + (lane >> 4) * 2 * 1024) : kOOB;
     }
+    // activations (E4M3, without DYN): row lane%16, k offset (lane/16)*32 of a K block
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, DYN ? 0 : (int)((g.M - 1) * g.lda + g.K), kRsrcFlags);
+    const uint32_t a_row_off = (uint32_t)(arow * g.lda) + (uint32_t)(lane >> 4) * 32;
 
     v4f acc[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // Register double buffer: the loads of the next UNROLL K blocks are in
-    // flight while the current ones are converted and multiplied.
     struct Frag {
         u4 alo[UNROLL], ahi[UNROLL], blo[UNROLL][NB], bhi[UNROLL][NB];
     };
@@ -117,17 +133,18 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
             const bool in = kb < kb_end;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                const uint8_t *p = b_ptr[j] + (int64_t)kb * 8 * 1024;
-                bool ok = in && b_ok[j];
-                f.blo[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(p)) : u4{0, 0, 0, 0};
-                f.bhi[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(p + 1024)) : u4{0, 0, 0, 0};
+                const uint32_t o = (in & (b_off[j] != kOOB)) ? b_off[j] + (uint32_t)kb * 8 * 1024 : kOOB;
+                f.blo[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)o, 0, kNT);
+                f.bhi[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)(o == kOOB ? kOOB : o + 1024), 0, kNT);
             }
             if constexpr (!DYN) {
-                const int64_t k = (int64_t)kb * 128 + (lane >> 4) * 32;
-                const bool ok_lo = in && a_ok && k < g.K;
-                const bool ok_hi = in && a_ok && k + 16 < g.K;
-                f.alo[u] = ok_lo ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128) : u4{0, 0, 0, 0};
-                f.ahi[u] = ok_hi ? *reinterpret_cast<const u4 *>(a_ptr + (int64_t)kb * 128 + 16) : u4{0, 0, 0, 0};
+                const uint32_t k = (uint32_t)kb * 128 + (uint32_t)(lane >> 4) * 32;  // K < 2^31
+                const uint32_t o = a_row_off + (uint32_t)kb * 128;
+                const bool ok = in & a_ok;
+                const uint32_t o_lo = (ok & (k < (uint32_t)g.K)) ? o : kOOB;
+                const uint32_t o_hi = (ok & (k + 16 < (uint32_t)g.K)) ? o + 16 : kOOB;
+                f.alo[u] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_lo, 0, 0);
+                f.ahi[u] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_hi, 0, 0);
             }
         }
     };
@@ -143,9 +160,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
             f.ahi[u] = ok ? *reinterpret_cast<const u4 *>(p + 16) : u4{0, 0, 0, 0};
         }
     };
-    auto compute = [&](const Frag &f) {
+    // blocks past the wavefront's range hold zeros and are skipped (a
+    // uniform branch around the MFMAs only)
+    auto compute = [&](const Frag &f, int kb0) {
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
+            if (kb0 + u >= kb_end) continue;
             if constexpr (EXACT) {
                 const uint32_t aw[8] = {f.alo[u].x, f.alo[u].y, f.alo[u].z, f.alo[u].w,
                                         f.ahi[u].x, f.ahi[u].y, f.ahi[u].z, f.ahi[u].w};
@@ -169,12 +189,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
             }
         }
     };
-    // PF register buffers of K blocks: the loads of PF-1 blocks are in flight
-    // while one is converted and multiplied (DYN: the first two are issued
-    // before the activation pass; a deeper prefetch measured slower).
-    constexpr int PF = 2;
+    // Ring of PF register buffers of UNROLL K blocks: the loads of PF-1
+    // buffers are in flight while one is converted and multiplied.
+    constexpr int PF = LCML_SKINNY_PF;
     Frag fr[PF];
-    Frag &f0 = fr[0], &f1 = fr[1];
     // DYN: the activations as float4 groups i = r * kq + c (K % 16 == 0); UQ
     // loads per thread are issued together, so one pass costs about one
     // memory round trip per UQ * 512 groups.  The first round is issued ahead
@@ -183,37 +201,37 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     constexpr int UQ = 8;
     const uint32_t kq = (uint32_t)(g.K / 4);
     const uint32_t nq = (uint32_t)g.M * kq;
+    const __amdgpu_buffer_rsrc_t x_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)g.x, 0, DYN ? (int)(((g.M - 1) * g.ldx + g.K) * 4) : 0, kRsrcFlags);
     auto xq = [&](uint32_t i) {
         const uint32_t r = i / kq;
-        return reinterpret_cast<const f4 *>(g.x + (int64_t)r * g.ldx)[i - r * kq];
+        const uint32_t o = i < nq ? (r * (uint32_t)g.ldx + (i - r * kq) * 4) * 4 : kOOB;
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
     };
     f4 v[UQ];
     if constexpr (DYN) {
 #pragma unroll
-        for (int u = 0; u < UQ; ++u) {
-            const uint32_t i = u * NT + tid;
-            v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int u = 0; u < UQ; ++u) v[u] = xq(u * NT + tid);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (kb_begin < kb_end) load(f0, kb_begin);
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        load(fr[p], kb_begin + p * UNROLL);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     float a_dyn = 1.0f;
     if constexpr (DYN) {
-#pragma unroll
-        for (int p = 1; p < PF; ++p)
-            if (kb_begin + p * UNROLL < kb_end) load(fr[p], kb_begin + p * UNROLL);
         __shared__ float wmax[WAVES];
         float m = 0.0f;
         for (uint32_t base = 0; base < nq; base += NT * UQ) {
             if (base) {
 #pragma unroll
-                for (int u = 0; u < UQ; ++u) {
-                    const uint32_t i = base + u * NT + tid;
-                    v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
-                }
+                for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
             }
 #pragma unroll
             for (int u = 0; u < UQ; ++u) {
-                // NaN compares false and is skipped, as in the standalone amax
+                // zeros past the end; NaN compares false and is skipped, as
+                // in the standalone amax
                 const float ax = fabsf(v[u].x), ay = fabsf(v[u].y), az = fabsf(v[u].z), aw = fabsf(v[u].w);
                 m = ax > m ? ax : m; m = ay > m ? ay : m; m = az > m ? az : m; m = aw > m ? aw : m;
             }
@@ -243,10 +261,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         } else {
             for (uint32_t base = 0; base < nq; base += NT * UQ) {
 #pragma unroll
-                for (int u = 0; u < UQ; ++u) {
-                    const uint32_t i = base + u * NT + tid;
-                    v[u] = i < nq ? xq(i) : f4{0.f, 0.f, 0.f, 0.f};
-                }
+                for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
 #pragma unroll
                 for (int u = 0; u < UQ; ++u) {
                     const uint32_t i = base + u * NT + tid;
@@ -261,25 +276,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         }
         __syncthreads();
     }
-    if constexpr (DYN) {
-        // ring of PF register buffers: consume block kb, refill with kb + PF
-        for (int kb0 = kb_begin; kb0 < kb_end; kb0 += PF * UNROLL) {
+    // consume buffer p (blocks kb), refill it with the blocks PF*UNROLL ahead
+    // (past the end: zeros, no memory traffic).  The scheduling barriers keep
+    // each buffer's loads together and in ring order, so the wait before a
+    // buffer's first use leaves the other PF-1 buffers' loads in flight.
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += PF * UNROLL) {
 #pragma unroll
-            for (int p = 0; p < PF; ++p) {
-                const int kb = kb0 + p * UNROLL;
-                if (kb < kb_end) {
-                    read_a(fr[p], kb);
-                    compute(fr[p]);
-                    if (kb + PF * UNROLL < kb_end) load(fr[p], kb + PF * UNROLL);
-                }
-            }
-        }
-    } else {
-        for (int kb0 = kb_begin; kb0 < kb_end; kb0 += 2 * UNROLL) {
-            if (kb0 + UNROLL < kb_end) load(f1, kb0 + UNROLL);
-            compute(f0);
-            if (kb0 + 2 * UNROLL < kb_end) load(f0, kb0 + 2 * UNROLL);
-            if (kb0 + UNROLL < kb_end) compute(f1);
+        for (int p = 0; p < PF; ++p) {
+            const int kb = kb0 + p * UNROLL;
+            if constexpr (DYN) read_a(fr[p], kb);
+            compute(fr[p], kb);
+            __builtin_amdgcn_sched_barrier(0);
+            load(fr[p], kb + PF * UNROLL);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
