@@ -213,7 +213,7 @@ def main() -> int:
         "config": {"workload": "small-M FP8 linear: x[M,4096] fp32 -> dynamic per-tensor E4M3 -> "
                                "x W[4096,11008] E4M3 (per-channel scales) -> bf16, M in {1,4,16}, "
                                "one step = the three linears (lcml_fp8_gemm_dynamic each: one fused launch "
-                               "for M*K <= 8192, else quantize + GEMM), timed as one HIP-graph replay",
+                               "for M*K <= 16384, else quantize + GEMM), timed as one HIP-graph replay",
                    "K": K, "N": N, "M": list(SMALL_MS), "weight_copies_rotated": N_WEIGHT_COPIES,
                    "bytes_per_step": bytes_step, "pct_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm",

@@ -172,7 +172,7 @@ LCML_API int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, in
  * With kernel LCML_KERNEL_SKINNY or SKINNY_FP8, M <= 16, x 16-byte aligned,
  * ldx % 4 == 0 and M * (K rounded up to 128, + 16) <= 96 KiB, one fused
  * kernel quantises x on the fly and needs no workspace; LCML_KERNEL_AUTO
- * fuses under the same conditions when also M * K <= 8192 (each workgroup
+ * fuses under the same conditions when also M * K <= 16384 (each workgroup
  * of the fused kernel encodes all of x).  Otherwise x must be
  * contiguous (ldx == K) and the call quantises into `workspace`
  * (lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel) bytes) and runs the

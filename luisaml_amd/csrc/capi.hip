@@ -193,8 +193,9 @@ namespace {
 // The fused kernel applies when the quantised activations fit its LDS copy.
 // Every workgroup of it reads and encodes all M*K activations; on the
 // 4096x11008 linear that redundant pass beats the separate quantise launch
-// up to M = 2, so AUTO fuses while M*K <= 8192.
-constexpr int64_t kAutoFuseMaxElems = 8192;
+// up to M = 4 (13.9 us against 15.6 us; at M = 8 it loses, 18.6 against
+// 16 us), so AUTO fuses while M*K <= 16384.
+constexpr int64_t kAutoFuseMaxElems = 16384;
 bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kernel) {
     const bool fits = M <= 16 && lcml::skinny_dynamic_lds_bytes(M, K) <= lcml::kSkinnyDynLdsMax &&
                       (!x || aligned(x, 16)) && ldx % 4 == 0 && ((M - 1) * ldx + K) * 4 < (int64_t)0x80000000;

@@ -74,13 +74,20 @@ __global__ __launch_bounds__(kThreads) void k_quantize_nchw_to_nhwc(const float 
         s = scale[0];
     }
     const Recip d = make_recip(s);
+    auto encode = [&](auto fast) {  // the scale's range test is uniform: one branch
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int cq = threadIdx.x / kPQ + CQP * j;
+        for (int j = 0; j < J; ++j) {
+            const int cq = threadIdx.x / kPQ + CQP * j;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            tile[(4 * pq + e) * PITCH + cq] = quantize4(v[j][0][e], v[j][1][e], v[j][2][e], v[j][3][e], d);
-    }
+            for (int e = 0; e < 4; ++e)
+                tile[(4 * pq + e) * PITCH + cq] =
+                    quantize4_t<decltype(fast)::value>(v[j][0][e], v[j][1][e], v[j][2][e], v[j][3][e], d);
+        }
+    };
+    if (d.fast)
+        encode(std::true_type{});
+    else
+        encode(std::false_type{});
     __syncthreads();
     constexpr int CHUNKS = CT / 16;  // 16-byte pieces per pixel
     uint8_t *yn = y + (int64_t)n * HW * C;

@@ -203,9 +203,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     const uint32_t nq = (uint32_t)g.M * kq;
     const __amdgpu_buffer_rsrc_t x_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.x, 0, DYN ? (int)(((g.M - 1) * g.ldx + g.K) * 4) : 0, kRsrcFlags);
+    // group i -> (row r, float4 c): i < 2^24, so the float quotient is off
+    // by at most one and two compares fix it (no integer division)
+    const float inv_kq = 1.0f / (float)kq;
+    auto split = [&](uint32_t i, uint32_t &r, uint32_t &c) {
+        uint32_t rr = (uint32_t)((float)i * inv_kq);
+        int cc = (int)i - (int)(rr * kq);
+        if (cc < 0) { --rr; cc += (int)kq; }
+        if (cc >= (int)kq) { ++rr; cc -= (int)kq; }
+        r = rr; c = (uint32_t)cc;
+    };
     auto xq = [&](uint32_t i) {
-        const uint32_t r = i / kq;
-        const uint32_t o = i < nq ? (r * (uint32_t)g.ldx + (i - r * kq) * 4) * 4 : kOOB;
+        uint32_t r, c;
+        split(i, r, c);
+        const uint32_t o = i < nq ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
         return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
     };
     f4 v[UQ];
@@ -248,27 +259,36 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         a_dyn = scale_from_amax_bits(f32_bits(m));
         if (g.scale_out && blockIdx.x == 0 && tid == 0) *g.scale_out = a_dyn;
         const Recip d = make_recip(a_dyn);
-        auto put = [&](uint32_t i, f4 x4) {
-            const uint32_t r = i / kq;
-            reinterpret_cast<uint32_t *>(a_lds + r * pitch)[i - r * kq] = quantize4(x4.x, x4.y, x4.z, x4.w, d);
-        };
-        if (nq <= NT * UQ) {  // one round: the values are still in registers
-#pragma unroll
-            for (int u = 0; u < UQ; ++u) {
-                const uint32_t i = u * NT + tid;
-                if (i < nq) put(i, v[u]);
-            }
-        } else {
-            for (uint32_t base = 0; base < nq; base += NT * UQ) {
-#pragma unroll
-                for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
+        // the scale's range test is uniform: one branch outside the loops
+        auto encode_all = [&](auto fast) {
+            auto put = [&](uint32_t i, f4 x4) {
+                uint32_t r, c;
+                split(i, r, c);
+                reinterpret_cast<uint32_t *>(a_lds + r * pitch)[c] =
+                    quantize4_t<decltype(fast)::value>(x4.x, x4.y, x4.z, x4.w, d);
+            };
+            if (nq <= NT * UQ) {  // one round: the values are still in registers
 #pragma unroll
                 for (int u = 0; u < UQ; ++u) {
-                    const uint32_t i = base + u * NT + tid;
+                    const uint32_t i = u * NT + tid;
                     if (i < nq) put(i, v[u]);
                 }
+            } else {
+                for (uint32_t base = 0; base < nq; base += NT * UQ) {
+#pragma unroll
+                    for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
+#pragma unroll
+                    for (int u = 0; u < UQ; ++u) {
+                        const uint32_t i = base + u * NT + tid;
+                        if (i < nq) put(i, v[u]);
+                    }
+                }
             }
-        }
+        };
+        if (d.fast)
+            encode_all(std::true_type{});
+        else
+            encode_all(std::false_type{});
         const uint32_t zq = (uint32_t)(pitch - 16) / 4 - kq;  // zero words per row for K <= k < Kp
         for (uint32_t i = tid; i < (uint32_t)g.M * zq; i += NT) {
             const uint32_t r = i / zq;

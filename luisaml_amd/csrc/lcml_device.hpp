@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace lcml {
 
 __host__ __device__ inline uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
@@ -88,14 +90,24 @@ __device__ inline Recip make_recip(float s) {
     return d;
 }
 
-__device__ inline float div_by(float x, const Recip &d) {
-    if (!d.fast) return __fdiv_rn(x, d.s);
+// x / s for d.fast scales.  The IEEE fallback for a tiny q0 sits under a
+// wavefront-uniform branch (ballot) that the empty volatile asm keeps the
+// compiler from if-converting (it would otherwise run the division sequence
+// for every element and select), so the common case costs three VALU
+// operations and a few compares.
+__device__ inline float div_fast(float x, const Recip &d) {
     const float q0 = x * d.r;
     float q = fmaf(fmaf(-q0, d.s, x), d.r, q0);
-    if (q0 != 0.0f && fabsf(q0) < 0x1p-100f) q = __fdiv_rn(x, d.s);
+    const bool tiny = q0 != 0.0f && fabsf(q0) < 0x1p-100f;
+    if (__builtin_amdgcn_ballot_w64(tiny) != 0) {
+        asm volatile("");
+        if (tiny) q = __fdiv_rn(x, d.s);
+    }
     if (fabsf(q0) == __builtin_inff()) q = q0;
     return q;
 }
+
+__device__ inline float div_by(float x, const Recip &d) { return d.fast ? div_fast(x, d) : __fdiv_rn(x, d.s); }
 
 // dynamic per-tensor scale from the fp32 bits of amax = max |x| over the
 // non-NaN elements: amax / 448, or 1 when that is not a positive finite number
@@ -144,9 +156,18 @@ __device__ inline float scale_from_partials(const uint32_t *part, int npart, flo
     return scale_from_amax_bits(f32_bits(block_max<THREADS>(m, red)));
 }
 
-// four consecutive elements quantised with one scale -> four packed codes
+// four consecutive elements quantised with one scale -> four packed codes;
+// quantize4_t<FAST> is for loops that test d.fast once outside
+template <bool FAST>
+__device__ inline uint32_t quantize4_t(float a, float b, float c, float e, const Recip &d) {
+    if constexpr (FAST)
+        return e4m3x2_hw(div_fast(a, d), div_fast(b, d)) | (e4m3x2_hw(div_fast(c, d), div_fast(e, d)) << 16);
+    else
+        return e4m3x2_hw(__fdiv_rn(a, d.s), __fdiv_rn(b, d.s)) | (e4m3x2_hw(__fdiv_rn(c, d.s), __fdiv_rn(e, d.s)) << 16);
+}
+
 __device__ inline uint32_t quantize4(float a, float b, float c, float e, const Recip &d) {
-    return e4m3x2_hw(div_by(a, d), div_by(b, d)) | (e4m3x2_hw(div_by(c, d), div_by(e, d)) << 16);
+    return d.fast ? quantize4_t<true>(a, b, c, e, d) : quantize4_t<false>(a, b, c, e, d);
 }
 
 // fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.

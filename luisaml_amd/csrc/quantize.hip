@@ -60,21 +60,34 @@ __global__ __launch_bounds__(kThreads) void k_quantize_vec(const float *__restri
         s_tensor = scale[0];
     }
     const Recip d_tensor = make_recip(s_tensor);
-    for (; i0 < n4; i0 += stride) {
-        uint32_t code[kU];
+    // per-tensor: the scale's range test is uniform, one branch outside the
+    // loop; per-axis: a scale (and its test) per float4
+    auto run = [&](auto mode) {
+        constexpr int MODE = decltype(mode)::value;  // 0: per-axis, 1: tensor fast, 2: tensor IEEE
+        for (; i0 < n4; i0 += stride) {
+            uint32_t code[kU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t i = i0 + (int64_t)u * kThreads;
-            const Recip d = (!FROM_AMAX && axis_len != 1) ? make_recip(scale[((i * 4) / inner) % axis_len]) : d_tensor;
-            code[u] = enc4(v[u], d);
-        }
-        if (i0 + stride < n4) load(i0 + stride);
+            for (int u = 0; u < kU; ++u) {
+                const int64_t i = i0 + (int64_t)u * kThreads;
+                if constexpr (MODE == 0)
+                    code[u] = enc4(v[u], make_recip(scale[((i * 4) / inner) % axis_len]));
+                else
+                    code[u] = quantize4_t<MODE == 1>(v[u].x, v[u].y, v[u].z, v[u].w, d_tensor);
+            }
+            if (i0 + stride < n4) load(i0 + stride);
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t i = i0 + (int64_t)u * kThreads;
-            if (i < n4) y4[i] = code[u];
+            for (int u = 0; u < kU; ++u) {
+                const int64_t i = i0 + (int64_t)u * kThreads;
+                if (i < n4) y4[i] = code[u];
+            }
         }
-    }
+    };
+    if (!FROM_AMAX && axis_len != 1)
+        run(std::integral_constant<int, 0>{});
+    else if (d_tensor.fast)
+        run(std::integral_constant<int, 1>{});
+    else
+        run(std::integral_constant<int, 2>{});
 }
 
 // Scalar path: any alignment, any per-axis layout, and the vector tail.

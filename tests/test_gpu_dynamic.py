@@ -116,8 +116,8 @@ def test_workspace_path(dev, M, kernel):
 def test_fused_limits_and_errors(dev):
     K = 8192
     ws = capi.lib().lcml_fp8_gemm_dynamic_workspace_bytes
-    assert ws(2, 4096, capi.KERNEL_AUTO) == 0 and ws(16, 4096, capi.KERNEL_SKINNY) == 0
-    assert ws(4, 4096, capi.KERNEL_AUTO) > 0  # AUTO: the separate quantise kernel is cheaper
+    assert ws(4, 4096, capi.KERNEL_AUTO) == 0 and ws(16, 4096, capi.KERNEL_SKINNY) == 0
+    assert ws(8, 4096, capi.KERNEL_AUTO) > 0  # AUTO: the separate quantise kernel is cheaper
     assert ws(16, K, capi.KERNEL_SKINNY) > 0  # LDS copy too large
     qw, sw, bp, d_sw = weights(K, 64, 30, dev)
     x = to_dev(synth.normal(31, (16, K)), dev)
