@@ -235,6 +235,31 @@ def main() -> int:
     })
     del g_steps, g_gemm, g_two
 
+    # same-box yardstick: the vendor library (hipBLASLt through torch) on the
+    # same small-M shape, E4M3 activations already quantised, per-tensor
+    # scales, bf16 out, the same seven rotated weight copies
+    lib_ref = {"note": "hipBLASLt via torch on this GPU: fp8 torch._scaled_mm (per-tensor scales, activations "
+                       "already E4M3) and bf16 torch.matmul; a yardstick, not the reference implementation"}
+    try:
+        w8 = [torch.from_numpy(np.ascontiguousarray(w.T)).to(dev).to(torch.float8_e4m3fn)
+              for _ in range(N_WEIGHT_COPIES)]  # [N, K]
+        one = torch.ones((), dtype=torch.float32, device=dev)
+        fp8_us = {}
+        for M in SMALL_MS:
+            x8 = xs[M].to(torch.float8_e4m3fn)
+            gl = capture(lambda i, x8=x8: torch._scaled_mm(x8, w8[i % N_WEIGHT_COPIES].t(), scale_a=one,
+                                                           scale_b=one, out_dtype=torch.bfloat16), 3 * args.steps)
+            gl.replay()
+            fp8_us[str(M)] = round(1e3 * timed(gl.replay) / (3 * args.steps), 2)
+            del gl
+        lib_ref["small_m_fp8_scaled_mm_us"] = fp8_us
+        lib_ref["small_m_fp8_scaled_mm_gbs"] = {m: round(gemm_kernel_bytes(int(m)) / (t * 1e-6) / 1e9, 1)
+                                                for m, t in fp8_us.items()}
+        del w8
+    except Exception as exc:  # an older torch without ROCm fp8 GEMM
+        lib_ref["small_m_error"] = f"{type(exc).__name__}: {str(exc)[:120]}"
+    out["library_reference"] = lib_ref
+
     # ------------------------------------------------------------ 8192^3 ---
     if not args.no_big:
         a = torch.from_numpy(synth.normal(301, (BIG, BIG))).to(dev)
@@ -275,6 +300,22 @@ def main() -> int:
             big[name] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
                          "pct_fp8_peak": round(100 * tflops / FP8_PEAK_TFLOPS, 1),
                          "pct_instruction_peak": round(100 * tflops / peak, 1)}
+        try:
+            ab = qa.view(torch.float8_e4m3fn).to(torch.bfloat16)
+            bb = ab.t().contiguous()
+            n = max(3, args.steps // 2)
+            torch.matmul(ab, bb)
+            ms_b = timed(lambda: [torch.matmul(ab, bb) for _ in range(n)]) / n
+            a8, b8 = qa.view(torch.float8_e4m3fn), qa.view(torch.float8_e4m3fn).t().contiguous().t()
+            one = torch.ones((), dtype=torch.float32, device=dev)
+            torch._scaled_mm(a8, b8, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            ms_8 = timed(lambda: [torch._scaled_mm(a8, b8, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+                                  for _ in range(n)]) / n
+            out["library_reference"]["gemm_8192_bf16_matmul_tflops"] = round(2.0 * BIG ** 3 / (ms_b * 1e-3) / 1e12, 1)
+            out["library_reference"]["gemm_8192_fp8_scaled_mm_tflops"] = round(2.0 * BIG ** 3 / (ms_8 * 1e-3) / 1e12, 1)
+            del ab, bb, a8, b8
+        except Exception as exc:
+            out["library_reference"]["gemm_8192_error"] = f"{type(exc).__name__}: {str(exc)[:120]}"
         out["gemm_8192"] = {"workload": "8192^3 E4M3 x E4M3, per-tensor scales, fp32 accumulate, bf16 out",
                             "default_kernel": "exact_bf16_mfma", **big,
                             "roofline": {"bound": "mfma", "achieved": big["exact_bf16_mfma"]["tflops"],
