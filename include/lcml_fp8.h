@@ -52,6 +52,7 @@ extern "C" {
 #define LCML_DTYPE_FLOAT 1
 #define LCML_DTYPE_BFLOAT16 16
 #define LCML_DTYPE_FLOAT8E4M3FN 17
+#define LCML_DTYPE_FLOAT8E5M2 19
 
 /* fused epilogue activations */
 #define LCML_ACT_NONE 0
@@ -288,6 +289,54 @@ LCML_API int lcml_fp8_sgemm(int64_t M, int64_t N, int64_t K, const float *a, int
  * 84-91, 122-126); act is LCML_ACT_*.  y may equal x.
  */
 LCML_API int lcml_fp8_activation(const float *x, float *y, int64_t n, int act, void *stream);
+
+/*
+ * Cast between LCML_DTYPE_FLOAT, FLOAT8E4M3FN and FLOAT8E5M2 (n elements;
+ * x and y may not overlap unless equal in size per element and identical).
+ * float -> fp8: the reference's CPU encoders, FP8E4M3FN::from_float
+ * (saturating to +-448) and FP8E5M2::from_float (|x| > 57344 -> +-inf),
+ * include/onnx/fp_quantized.h:149-223, 272-346; fp8 -> float: to_float
+ * (226-249, 350-377); fp8 -> fp8 through the exact float value.  Replaces
+ * Cast::apply's fp8 branches (src/onnx/operators/cast.cpp:39-77), whose
+ * float -> fp8 direction goes through half first; `saturate` is not an
+ * argument because that op reads it only for float -> int (cast.cpp:86-98).
+ */
+LCML_API int lcml_fp8_cast(const void *x, int x_dtype, void *y, int y_dtype, int64_t n, void *stream);
+
+/*
+ * QuantizeLinear / DequantizeLinear with a FLOAT8E5M2 tensor (ONNX opset 21,
+ * zero point 0), same [outer, axis_len, inner] view as lcml_fp8_quantize:
+ *   y = from_float_e5m2(x / y_scale) (IEEE fp32 divide), where saturate = 1
+ *       first clamps |x / y_scale| > 57344 (inf included) to +-57344 and
+ *       saturate = 0 keeps the encoder's +-inf;
+ *   y = to_float_e5m2(x) * x_scale.
+ * No counterpart in the reference (its loader rejects both ops,
+ * src/onnx/onnx.cpp:228-229); the numeric core is FP8E5M2.
+ */
+LCML_API int lcml_fp8_quantize_e5m2(const float *x, uint8_t *y, int64_t outer, int64_t axis_len, int64_t inner,
+                                    const float *y_scale, int saturate, void *stream);
+LCML_API int lcml_fp8_dequantize_e5m2(const uint8_t *x, float *y, int64_t outer, int64_t axis_len,
+                                      int64_t inner, const float *x_scale, void *stream);
+
+/*
+ * Elementwise binary op, y = a OP b, with numpy broadcasting (shapes are
+ * right-aligned, size-1 dimensions broadcast; y_shape must be the
+ * broadcast shape; at most 8 dimensions; shapes are HOST arrays, data
+ * device pointers).  dtype: LCML_DTYPE_FLOAT (the op in fp32),
+ * FLOAT8E4M3FN or FLOAT8E5M2 (all three tensors of that type): as the
+ * reference's Binary ops on quantised tensors
+ * (src/onnx/operators/binary.cpp:184-285), both operands are decoded, the
+ * op is rounded to half precision (the reference computes in half) and the
+ * result is encoded with the format's from_float.
+ * Replaces Add / Sub / Mul / Div (binary.cpp:335-345) on the fp8 path.
+ */
+#define LCML_BINARY_ADD 0
+#define LCML_BINARY_SUB 1
+#define LCML_BINARY_MUL 2
+#define LCML_BINARY_DIV 3
+LCML_API int lcml_fp8_binary(int op, int dtype, const void *a, const int64_t *a_shape, int a_ndim, const void *b,
+                             const int64_t *b_shape, int b_ndim, void *y, const int64_t *y_shape, int y_ndim,
+                             void *stream);
 
 #ifdef __cplusplus
 }

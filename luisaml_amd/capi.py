@@ -17,7 +17,8 @@ LIB_PATH = os.path.join(HERE, "liblcml_fp8.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lcml_fp8.h")
 
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
-DTYPE_FLOAT, DTYPE_BFLOAT16, DTYPE_FLOAT8E4M3FN = 1, 16, 17
+DTYPE_FLOAT, DTYPE_BFLOAT16, DTYPE_FLOAT8E4M3FN, DTYPE_FLOAT8E5M2 = 1, 16, 17, 19
+BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_MFMA, KERNEL_SKINNY, KERNEL_VALU, KERNEL_MFMA_FP8, KERNEL_SKINNY_FP8 = 0, 1, 2, 3, 4, 5
 DYNAMIC_WORKSPACE_BYTES = 4096
@@ -50,6 +51,11 @@ _SIGS = {
     "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
                                      _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
     "lcml_fp8_quantize_nhwc": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "lcml_fp8_cast": (_int, [_vp, _int, _vp, _int, _i64, _vp]),
+    "lcml_fp8_quantize_e5m2": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
+    "lcml_fp8_dequantize_e5m2": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "lcml_fp8_binary": (_int, [_int, _int, _vp, C.POINTER(C.c_int64), _int, _vp, C.POINTER(C.c_int64), _int,
+                               _vp, C.POINTER(C.c_int64), _int, _vp]),
     "lcml_fp8_packed_conv_weight_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "lcml_fp8_pack_conv_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "lcml_fp8_conv2d": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
@@ -348,4 +354,50 @@ def activation(x: torch.Tensor, act: int, out: torch.Tensor | None = None, strea
     assert x.dtype == torch.float32 and x.is_contiguous()
     y = out if out is not None else torch.empty_like(x)
     _check(lib().lcml_fp8_activation(_ptr(x), _ptr(y), x.numel(), int(act), _stream(stream)))
+    return y
+
+
+# ---------------------------------------------------- fp8 data-type ops ----
+
+def cast(x: torch.Tensor, x_dtype: int, y_dtype: int, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Cast between DTYPE_FLOAT (float32 tensor) and DTYPE_FLOAT8E4M3FN /
+    DTYPE_FLOAT8E5M2 (uint8 code tensors)."""
+    assert x.is_contiguous()
+    tdt = torch.float32 if y_dtype == DTYPE_FLOAT else torch.uint8
+    y = out if out is not None else torch.empty(x.shape, dtype=tdt, device=x.device)
+    _check(lib().lcml_fp8_cast(_ptr(x), int(x_dtype), _ptr(y), int(y_dtype), x.numel(), _stream(stream)))
+    return y
+
+
+def quantize_e5m2(x: torch.Tensor, scale: torch.Tensor, axis: int = 1, saturate: int = 1,
+                  out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """QuantizeLinear fp32 -> E5M2 codes (uint8)."""
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    scale = scale.reshape(-1)
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    o, a, i = _axis_view(tuple(x.shape), axis, scale.numel())
+    _check(lib().lcml_fp8_quantize_e5m2(_ptr(x), _ptr(y), o, a, i, _ptr(scale), int(saturate), _stream(stream)))
+    return y
+
+
+def dequantize_e5m2(q: torch.Tensor, scale: torch.Tensor, axis: int = 1, out: torch.Tensor | None = None,
+                    stream=None) -> torch.Tensor:
+    assert q.dtype == torch.uint8 and q.is_contiguous()
+    scale = scale.reshape(-1)
+    y = out if out is not None else torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    o, a, i = _axis_view(tuple(q.shape), axis, scale.numel())
+    _check(lib().lcml_fp8_dequantize_e5m2(_ptr(q), _ptr(y), o, a, i, _ptr(scale), _stream(stream)))
+    return y
+
+
+def binary(op: int, a: torch.Tensor, b: torch.Tensor, dtype: int, out: torch.Tensor | None = None,
+           stream=None) -> torch.Tensor:
+    """y = a OP b with numpy broadcasting; dtype DTYPE_FLOAT (float32 tensors)
+    or DTYPE_FLOAT8E4M3FN / DTYPE_FLOAT8E5M2 (uint8 code tensors)."""
+    assert a.is_contiguous() and b.is_contiguous()
+    ys = tuple(torch.broadcast_shapes(a.shape, b.shape))
+    y = out if out is not None else torch.empty(ys, dtype=a.dtype, device=a.device)
+    sh = lambda t: (C.c_int64 * max(1, len(t)))(*t)
+    _check(lib().lcml_fp8_binary(int(op), int(dtype), _ptr(a), sh(tuple(a.shape)), a.dim(), _ptr(b),
+                                 sh(tuple(b.shape)), b.dim(), _ptr(y), sh(tuple(y.shape)), y.dim(), _stream(stream)))
     return y

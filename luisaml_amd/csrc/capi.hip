@@ -398,4 +398,82 @@ int lcml_fp8_activation(const float *x, float *y, int64_t n, int act, void *stre
     return hip_status(lcml::launch_activation(x, y, n, act, (hipStream_t)stream), "lcml_fp8_activation");
 }
 
+namespace {
+bool fp8_dtype_ok(int dt) {
+    return dt == LCML_DTYPE_FLOAT || dt == LCML_DTYPE_FLOAT8E4M3FN || dt == LCML_DTYPE_FLOAT8E5M2;
+}
+}  // namespace
+
+int lcml_fp8_cast(const void *x, int x_dtype, void *y, int y_dtype, int64_t n, void *stream) {
+    const char *fn = "lcml_fp8_cast";
+    if (n < 0) return fail(LCML_ERR_INVALID_ARG, "%s: n < 0", fn);
+    if (!fp8_dtype_ok(x_dtype) || !fp8_dtype_ok(y_dtype))
+        return fail(LCML_ERR_UNSUPPORTED, "%s: dtypes %d -> %d (FLOAT, FLOAT8E4M3FN, FLOAT8E5M2 only)", fn, x_dtype,
+                    y_dtype);
+    if (n == 0) return LCML_OK;
+    if (!x || !y) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (x_dtype == LCML_DTYPE_FLOAT ? !aligned(x, 4) : false) return fail(LCML_ERR_INVALID_ARG, "%s: x misaligned", fn);
+    if (y_dtype == LCML_DTYPE_FLOAT ? !aligned(y, 4) : false) return fail(LCML_ERR_INVALID_ARG, "%s: y misaligned", fn);
+    return hip_status(lcml::launch_cast(x, x_dtype, y, y_dtype, n, (hipStream_t)stream), fn);
+}
+
+int lcml_fp8_quantize_e5m2(const float *x, uint8_t *y, int64_t outer, int64_t axis_len, int64_t inner,
+                           const float *y_scale, int saturate, void *stream) {
+    if (int rc = check_view(outer, axis_len, inner, "lcml_fp8_quantize_e5m2")) return rc;
+    if (outer * axis_len * inner == 0) return LCML_OK;
+    if (!x || !y || !y_scale) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize_e5m2: NULL pointer");
+    if (saturate != 0 && saturate != 1) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_quantize_e5m2: saturate %d", saturate);
+    return hip_status(lcml::launch_quantize_e5m2(x, y, outer, axis_len, inner, y_scale, saturate == 1,
+                                                 (hipStream_t)stream),
+                      "lcml_fp8_quantize_e5m2");
+}
+
+int lcml_fp8_dequantize_e5m2(const uint8_t *x, float *y, int64_t outer, int64_t axis_len, int64_t inner,
+                             const float *x_scale, void *stream) {
+    if (int rc = check_view(outer, axis_len, inner, "lcml_fp8_dequantize_e5m2")) return rc;
+    if (outer * axis_len * inner == 0) return LCML_OK;
+    if (!x || !y || !x_scale) return fail(LCML_ERR_INVALID_ARG, "lcml_fp8_dequantize_e5m2: NULL pointer");
+    return hip_status(lcml::launch_dequantize_e5m2(x, y, outer, axis_len, inner, x_scale, (hipStream_t)stream),
+                      "lcml_fp8_dequantize_e5m2");
+}
+
+int lcml_fp8_binary(int op, int dtype, const void *a, const int64_t *a_shape, int a_ndim, const void *b,
+                    const int64_t *b_shape, int b_ndim, void *y, const int64_t *y_shape, int y_ndim, void *stream) {
+    const char *fn = "lcml_fp8_binary";
+    if (op < LCML_BINARY_ADD || op > LCML_BINARY_DIV) return fail(LCML_ERR_INVALID_ARG, "%s: op %d", fn, op);
+    if (!fp8_dtype_ok(dtype)) return fail(LCML_ERR_UNSUPPORTED, "%s: dtype %d", fn, dtype);
+    if (a_ndim < 0 || b_ndim < 0 || y_ndim < 0 || y_ndim > lcml::kMaxBcastDims || a_ndim > y_ndim || b_ndim > y_ndim)
+        return fail(LCML_ERR_INVALID_ARG, "%s: ranks a=%d b=%d y=%d (at most %d, y the largest)", fn, a_ndim, b_ndim,
+                    y_ndim, lcml::kMaxBcastDims);
+    if ((a_ndim && !a_shape) || (b_ndim && !b_shape) || (y_ndim && !y_shape))
+        return fail(LCML_ERR_INVALID_ARG, "%s: NULL shape", fn);
+    // numpy broadcasting, right-aligned; element strides of a and b per output dim
+    lcml::BcastGeom g{};
+    g.ndim = y_ndim;
+    int64_t n = 1, acc_a = 1, acc_b = 1;
+    bool same = a_ndim == y_ndim && b_ndim == y_ndim;
+    for (int d = y_ndim - 1; d >= 0; --d) {
+        const int da = d - (y_ndim - a_ndim), db = d - (y_ndim - b_ndim);
+        const int64_t ea = da >= 0 ? a_shape[da] : 1, eb = db >= 0 ? b_shape[db] : 1, ey = y_shape[d];
+        if (ea < 0 || eb < 0 || ey < 0) return fail(LCML_ERR_INVALID_ARG, "%s: negative dimension", fn);
+        const int64_t want = ea == 1 ? eb : (eb == 1 || eb == ea ? ea : -1);
+        if (want < 0 || want != ey)
+            return fail(LCML_ERR_INVALID_ARG, "%s: dim %d: a %lld, b %lld do not broadcast to y %lld", fn, d,
+                        (long long)ea, (long long)eb, (long long)ey);
+        same = same && ea == ey && eb == ey;
+        g.dims[d] = ey;
+        g.sa[d] = ea == 1 ? 0 : acc_a;
+        g.sb[d] = eb == 1 ? 0 : acc_b;
+        acc_a *= ea;
+        acc_b *= eb;
+        if (ey && n > ((int64_t)1 << 40) / ey) return fail(LCML_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+        n *= ey;
+    }
+    if (n == 0) return LCML_OK;
+    if (!a || !b || !y) return fail(LCML_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+    if (dtype == LCML_DTYPE_FLOAT && (!aligned(a, 4) || !aligned(b, 4) || !aligned(y, 4)))
+        return fail(LCML_ERR_INVALID_ARG, "%s: fp32 tensors must be 4-byte aligned", fn);
+    return hip_status(lcml::launch_fp8_binary(op, dtype, a, b, y, n, same, g, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

@@ -61,6 +61,23 @@ __device__ inline uint32_t e4m3x2_hw(float a, float b) {
     return v;
 }
 
+// Two fp32 values -> two E5M2 codes in bytes 0..1, as the reference's
+// FP8E5M2::from_float (include/onnx/fp_quantized.h:272-346): NaN -> 0x7f,
+// +-0 -> 0x00, |v| > 57344 and +-inf -> sign|0x7c (infinity: this encoder
+// does not saturate), otherwise round to nearest even with signed underflow.
+// The rounding is v_cvt_pk_bf8_f32 (OCP E5M2) on v + 0.0, which turns -0
+// into +0; NaN and the overflow range are selected explicitly.
+__device__ inline uint32_t e5m2_fix(float v, uint32_t hw) {
+    if (v != v) return 0x7fu;
+    if (fabsf(v) > 57344.0f) return v < 0.0f ? 0xfcu : 0x7cu;
+    return hw;
+}
+
+__device__ inline uint32_t e5m2x2_hw(float a, float b) {
+    const uint32_t v = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(a + 0.0f, b + 0.0f, 0, false);
+    return e5m2_fix(a, v & 0xffu) | (e5m2_fix(b, (v >> 8) & 0xffu) << 8);
+}
+
 // Division by a scale that is fixed for many elements, rounded exactly like
 // IEEE x / s.  With r = RN(1/s), q0 = RN(x*r) is within one ulp of x/s and
 // one Newton correction q = RN(q0 + RN(x - q0*s)*r) (the residual is exact

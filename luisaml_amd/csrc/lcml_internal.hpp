@@ -69,4 +69,21 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *bias, 
                              int group, int OH, int OW, int act, hipStream_t s);
 hipError_t launch_activation(const float *x, float *y, int64_t n, int act, hipStream_t s);
 
+// element formats of the fp8 data-type kernels (the ONNX type numbers)
+constexpr int kFmtFloat = 1, kFmtE4M3 = 17, kFmtE5M2 = 19;
+hipError_t launch_cast(const void *x, int x_fmt, void *y, int y_fmt, int64_t n, hipStream_t s);
+hipError_t launch_quantize_e5m2(const float *x, uint8_t *y, int64_t outer, int64_t axis_len, int64_t inner,
+                                const float *scale, bool saturate, hipStream_t s);
+hipError_t launch_dequantize_e5m2(const uint8_t *x, float *y, int64_t outer, int64_t axis_len, int64_t inner,
+                                  const float *scale, hipStream_t s);
+// y = a OP b with numpy broadcasting: out_dims[ndim], element strides of a
+// and b per output dim (0 where broadcast); ndim <= kMaxBcastDims
+constexpr int kMaxBcastDims = 8;
+struct BcastGeom {
+    int ndim;
+    int64_t dims[kMaxBcastDims], sa[kMaxBcastDims], sb[kMaxBcastDims];
+};
+hipError_t launch_fp8_binary(int op, int fmt, const void *a, const void *b, void *y, int64_t n, bool same_shape,
+                             const BcastGeom &g, hipStream_t s);
+
 }  // namespace lcml

@@ -65,6 +65,18 @@ def lib():
                                           C.c_float, C.c_float, f32p, C.c_int, i64, i64, f64p]),
             "orc_gemm_f64": (None, [i64, i64, i64, f32p, f32p, f64p]),
             "orc_conv2d": (None, [f32p, f32p, f32p, f32p] + [i64] * 16 + [C.c_int]),
+            "orc_e5m2_from_float": (C.c_uint8, [C.c_float]),
+            "orc_e5m2_to_float": (C.c_float, [C.c_uint8]),
+            "orc_e5m2_spec_encode": (C.c_uint8, [C.c_float]),
+            "orc_e5m2_encode_bits": (None, [C.c_uint32, C.c_uint64, u8p]),
+            "orc_e5m2_sweep_vs_spec": (C.c_uint64, [C.c_uint32, C.c_uint64, C.POINTER(C.c_uint32)]),
+            "orc_e5m2_decode_table": (None, [f32p]),
+            "orc_half_round": (C.c_float, [C.c_double]),
+            "orc_half_round_array": (None, [f32p, f32p, i64]),
+            "orc_fp8_binary": (None, [C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_int64), C.c_int, C.c_void_p,
+                                      C.POINTER(C.c_int64), C.c_int, C.c_void_p, C.POINTER(C.c_int64), C.c_int]),
+            "orc_quantize_e5m2": (None, [f32p, u8p, i64, i64, i64, f32p, C.c_int]),
+            "orc_dequantize_e5m2": (None, [u8p, f32p, i64, i64, i64, f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -295,3 +307,93 @@ def conv2d(X, W, bias=None, strides=(1, 1), pads=(0, 0), dilations=(1, 1), group
     lib().orc_conv2d(_p(X, C.c_float), _p(W, C.c_float), _p(b, C.c_float), _p(Y, C.c_float),
                      N, Cc, H, Wd, M, kH, kW, sH, sW, pH, pW, dH, dW, group, oH, oW, int(act))
     return Y
+
+
+# --------------------------------------------------------------- E5M2 -------
+
+DTYPE_FLOAT, DTYPE_E4M3, DTYPE_E5M2 = 1, 17, 19
+OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
+
+
+def e5m2_from_float(x) -> np.ndarray:
+    """Vectorised FP8E5M2::from_float (fp_quantized.h:272-346): no saturation."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, np.uint8)
+    one = np.ones(1, np.float32)
+    lib().orc_quantize_e5m2(_p(x.reshape(-1), C.c_float), _p(out.reshape(-1), C.c_uint8), 1, 1, x.size,
+                            _p(one, C.c_float), 0)
+    return out
+
+
+def e5m2_spec_encode(x: float) -> int:
+    return int(lib().orc_e5m2_spec_encode(float(x)))
+
+
+def e5m2_encode_bits(first: int, count: int) -> np.ndarray:
+    out = np.empty(count, np.uint8)
+    lib().orc_e5m2_encode_bits(first, count, _p(out, C.c_uint8))
+    return out
+
+
+def e5m2_sweep_vs_spec(first: int, count: int) -> tuple[int, int | None]:
+    bad_at = C.c_uint32(0)
+    n = lib().orc_e5m2_sweep_vs_spec(first, count, C.byref(bad_at))
+    return int(n), (int(bad_at.value) if n else None)
+
+
+def e5m2_decode_table() -> np.ndarray:
+    """FP8E5M2::to_float (fp_quantized.h:350-377) for all 256 codes."""
+    out = np.empty(256, np.float32)
+    lib().orc_e5m2_decode_table(_p(out, C.c_float))
+    return out
+
+
+def e5m2_to_float(q) -> np.ndarray:
+    return e5m2_decode_table()[np.asarray(q, dtype=np.uint8)]
+
+
+def half_round(x) -> np.ndarray:
+    """IEEE binary16 round-to-nearest-even of fp32 values, as fp32."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, np.float32)
+    lib().orc_half_round_array(_p(x.reshape(-1), C.c_float), _p(out.reshape(-1), C.c_float), x.size)
+    return out
+
+
+def quantize_e5m2(x, scale, axis: int = 1, saturate: int = 1) -> np.ndarray:
+    """QuantizeLinear to E5M2: from_float(x / scale), saturate=1 clamps to +-57344."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    s = np.ascontiguousarray(np.atleast_1d(np.asarray(scale, dtype=np.float32)))
+    o, a, i = _axis_view(x.shape, axis, s.size)
+    out = np.empty(x.shape, np.uint8)
+    lib().orc_quantize_e5m2(_p(x.reshape(-1), C.c_float), _p(out.reshape(-1), C.c_uint8), o, a, i,
+                            _p(s, C.c_float), int(saturate))
+    return out
+
+
+def dequantize_e5m2(q, scale, axis: int = 1) -> np.ndarray:
+    q = np.ascontiguousarray(np.asarray(q, dtype=np.uint8))
+    s = np.ascontiguousarray(np.atleast_1d(np.asarray(scale, dtype=np.float32)))
+    o, a, i = _axis_view(q.shape, axis, s.size)
+    out = np.empty(q.shape, np.float32)
+    lib().orc_dequantize_e5m2(_p(q.reshape(-1), C.c_uint8), _p(out.reshape(-1), C.c_float), o, a, i,
+                              _p(s, C.c_float))
+    return out
+
+
+def broadcast_shape(sa, sb):
+    return tuple(np.broadcast_shapes(tuple(sa), tuple(sb)))
+
+
+def fp8_binary(op: int, dtype: int, a, b) -> np.ndarray:
+    """Add/Sub/Mul/Div with numpy broadcasting: fp32 arithmetic for FLOAT,
+    decode -> op in half -> encode for E4M3 / E5M2 (binary.cpp:184-285)."""
+    npdt = np.float32 if dtype == DTYPE_FLOAT else np.uint8
+    a = np.ascontiguousarray(np.asarray(a, dtype=npdt))
+    b = np.ascontiguousarray(np.asarray(b, dtype=npdt))
+    ys = broadcast_shape(a.shape, b.shape)
+    y = np.empty(ys, npdt)
+    sh = lambda t: (C.c_int64 * max(1, len(t)))(*t)
+    lib().orc_fp8_binary(op, dtype, a.ctypes.data, sh(a.shape), a.ndim, b.ctypes.data, sh(b.shape), b.ndim,
+                         y.ctypes.data, sh(ys), len(ys))
+    return y

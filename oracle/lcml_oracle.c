@@ -1,5 +1,5 @@
 /*
- * lcml_oracle.c -- CPU oracle for the FP8 (E4M3) quantized-linear path.
+ * lcml_oracle.c -- CPU oracle for the FP8 (E4M3 / E5M2) quantized-linear path.
  *
  * TEST INFRASTRUCTURE ONLY.  This file restates, on the CPU, the arithmetic
  * of the reference ONNX runtime (LuisaGroup/LuisaML) that the HIP library in
@@ -38,6 +38,23 @@
  *                         half accumulation for fp8 inputs at conv.cpp:67-70)
  *   orc_bf16_rne          closed form: fp32 -> bf16 round to nearest even,
  *                         NaN kept quiet.  No counterpart in the reference.
+ *   orc_e5m2_from_float   include/onnx/fp_quantized.h:272-346  (line by line)
+ *   orc_e5m2_to_float     include/onnx/fp_quantized.h:350-377  (line by line)
+ *   orc_e5m2_spec_encode  closed-form specification of the above; pins it over
+ *                         all 2^32 fp32 bit patterns.
+ *   orc_half_round        IEEE binary16 round to nearest even (subnormals,
+ *                         overflow to inf): the precision of the reference's
+ *                         DSL arithmetic on decoded fp8 values (its decoders
+ *                         return half, fp_quantized.h:610, 721).
+ *   orc_fp8_binary        src/onnx/operators/binary.cpp:184-285 (quantised
+ *                         Add/Sub/Mul/Div: decode both operands to half, the
+ *                         op in half, encode) and 59-182 (numpy broadcasting);
+ *                         the encode is the CPU from_float of the half value.
+ *   orc_quantize_e5m2 / orc_dequantize_e5m2
+ *                         QuantizeLinear / DequantizeLinear with a
+ *                         FLOAT8E5M2 target (ONNX opset 21): from_float(x / s)
+ *                         with saturate=1 clamping |x / s| > 57344 (inf
+ *                         included) to +-57344; to_float(q) * s.
  *
  * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fopenmp -mavx2 -mfma).
  * -ffp-contract=off keeps every multiply and add separately rounded except
@@ -487,5 +504,228 @@ ORC_API void orc_conv2d(const float *X, const float *W, const float *bias, float
                     if (bias) sum += bias[m];
                     Y[((n * M + m) * oH + oh) * oW + ow] = apply_act(sum, act);
                 }
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* E5M2 codec                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Restatement of FP8E5M2::from_float, fp_quantized.h:272-346.  Unlike the
+ * E4M3 encoder it does not saturate: |v| > 57344 and +-inf give +-inf. */
+ORC_API uint8_t orc_e5m2_from_float(float v) {
+    const int kMantBits = 2, kBias = 15, kInfNanExp = 31;
+    const uint8_t kMantMask = 0x03, kSignMask = 0x80;
+    if (isnan(v)) return 0x7f;                        /* 274-277 */
+    if (isinf(v)) return v < 0.0f ? 0xfc : 0x7c;      /* 278-281 */
+    if (v == 0.0f) return 0;                          /* 282-285 (-0.0 -> 0x00) */
+    uint32_t sign = 0;
+    if (v < 0.0f) { sign = 1; v = -v; }               /* 286-290 */
+    const float max_finite = 57344.0f;
+    if (v > max_finite) return sign ? 0xfc : 0x7c;    /* 292-297 */
+    int32_t exp;
+    float mant = frexpf(v, &exp);                     /* 299-304 */
+    mant *= 2.0f;
+    exp -= 1;
+    int32_t e = exp + kBias;                          /* 306 */
+    if (e <= 0) {                                     /* 307-317 */
+        if (e < -kMantBits) return sign ? kSignMask : 0;
+        int32_t shift = 1 - e;
+        mant = mant / (float)(1 << shift);
+        e = 0;
+    }
+    float mant_q = floorf(mant * (float)(1 << kMantBits)); /* 319-322 */
+    float frac = mant * (float)(1 << kMantBits) - mant_q;
+    uint8_t m = (uint8_t)((uint8_t)mant_q & kMantMask);
+    if (frac > 0.5f || (frac == 0.5f && (m & 1))) {   /* 324-331 */
+        m += 1;
+        if (m > kMantMask) { m = 0; e += 1; }
+    }
+    if (e >= kInfNanExp) { e = kInfNanExp; m = 0; }   /* 333-337 */
+    if (e == 0 && m == 0) return sign ? kSignMask : 0; /* 339-343 */
+    return (uint8_t)((sign ? kSignMask : 0) | (uint8_t)(e << kMantBits) | m);
+}
+
+/* Restatement of FP8E5M2::to_float, fp_quantized.h:350-377. */
+ORC_API float orc_e5m2_to_float(uint8_t bits) {
+    uint8_t sign = (bits & 0x80) >> 7;
+    uint8_t e = (bits >> 2) & 31;
+    uint8_t m = bits & 3;
+    if (e == 0 && m == 0) return sign ? -0.0f : 0.0f;
+    if (e == 31 && m == 0) return sign ? -INFINITY : INFINITY;
+    if (e == 31) return u2f(0x7fc00000u); /* quiet NaN */
+    float value;
+    if (e == 0)
+        value = (float)m / (float)(1 << 2) * powf(2.0f, (float)(1 - 15));
+    else
+        value = (1.0f + (float)m / (float)(1 << 2)) * powf(2.0f, (float)(e - 15));
+    return sign ? -value : value;
+}
+
+/*
+ * Closed-form specification of the E5M2 encoder, independent of the
+ * frexp/floor algorithm:
+ *   NaN -> 0x7f;  +-0 -> 0x00;  |x| > 57344 (incl. inf) -> sign|0x7c;
+ *   otherwise the E5M2 grid point nearest to |x|, ties to the even code;
+ *   a zero result keeps the sign (0x80).
+ */
+static double g_grid5[124]; /* positive finite codes 0x00..0x7b */
+static int g_grid5_ready = 0;
+static void grid5_init(void) {
+    if (g_grid5_ready) return;
+    for (int c = 0; c < 124; ++c) {
+        int e = c >> 2, m = c & 3;
+        g_grid5[c] = e == 0 ? ldexp((double)m, -16) : ldexp(1.0 + m / 4.0, e - 15);
+    }
+    g_grid5_ready = 1;
+}
+
+ORC_API uint8_t orc_e5m2_spec_encode(float x) {
+    uint32_t u = f2u(x);
+    uint32_t s = u >> 31, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7f;
+    if (a == 0) return 0x00;
+    double v = (double)u2f(a);
+    if (v > 57344.0) return (uint8_t)((s << 7) | 0x7c);
+    grid5_init();
+    int lo = 0, hi = 123;
+    while (hi - lo > 1) {
+        int mid = (lo + hi) / 2;
+        if (g_grid5[mid] <= v) lo = mid; else hi = mid;
+    }
+    int c;
+    double dlo = v - g_grid5[lo], dhi = g_grid5[hi] - v;
+    if (dlo < dhi) c = lo;
+    else if (dhi < dlo) c = hi;
+    else c = (lo & 1) ? hi : lo;
+    if (c == 0) return (uint8_t)(s << 7);
+    return (uint8_t)((s << 7) | c);
+}
+
+ORC_API void orc_e5m2_encode_bits(uint32_t first, uint64_t count, uint8_t *out) {
+    int nt = orc_get_threads();
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (int64_t i = 0; i < (int64_t)count; ++i)
+        out[i] = orc_e5m2_from_float(u2f(first + (uint32_t)i));
+}
+
+ORC_API uint64_t orc_e5m2_sweep_vs_spec(uint32_t first, uint64_t count, uint32_t *first_bad) {
+    grid5_init();
+    uint64_t bad = 0;
+    uint32_t lowest = 0xffffffffu;
+    int nt = orc_get_threads();
+#pragma omp parallel for num_threads(nt) schedule(static) reduction(+ : bad) reduction(min : lowest)
+    for (int64_t i = 0; i < (int64_t)count; ++i) {
+        uint32_t b = first + (uint32_t)i;
+        float x = u2f(b);
+        if (orc_e5m2_from_float(x) != orc_e5m2_spec_encode(x)) {
+            ++bad;
+            if (b < lowest) lowest = b;
+        }
+    }
+    if (bad && first_bad) *first_bad = lowest;
+    return bad;
+}
+
+ORC_API void orc_e5m2_decode_table(float *out256) {
+    for (int c = 0; c < 256; ++c) out256[c] = orc_e5m2_to_float((uint8_t)c);
+}
+
+/* x rounded once to IEEE binary16 (nearest, ties to even; subnormals with
+ * quantum 2^-24; |x| >= 65520 -> inf), returned as float (exact). */
+ORC_API float orc_half_round(double x) {
+    if (isnan(x)) return u2f(0x7fc00000u);
+    if (isinf(x)) return (float)x;
+    double a = fabs(x);
+    if (a >= 65520.0) return x < 0 ? -INFINITY : INFINITY;
+    if (a == 0.0) return (float)x;
+    int e;
+    frexp(a, &e);                 /* a = f * 2^e, f in [0.5, 1) */
+    int q = e - 1 - 10;           /* quantum exponent for 11 significant bits */
+    if (q < -24) q = -24;         /* subnormal quantum */
+    double r = rint(ldexp(a, -q)); /* default rounding mode: nearest, ties to even */
+    r = ldexp(r, q);
+    return (float)(x < 0 ? -r : r);
+}
+
+ORC_API void orc_half_round_array(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_half_round((double)x[i]);
+}
+
+/* dtype codes: the ONNX TensorProto numbers */
+#define ORC_FLOAT 1
+#define ORC_E4M3 17
+#define ORC_E5M2 19
+
+static inline float dec_any(const void *p, int64_t i, int dtype) {
+    if (dtype == ORC_FLOAT) return ((const float *)p)[i];
+    uint8_t c = ((const uint8_t *)p)[i];
+    return dtype == ORC_E4M3 ? orc_e4m3_to_float(c) : orc_e5m2_to_float(c);
+}
+
+/*
+ * Elementwise Add(0) / Sub(1) / Mul(2) / Div(3) with numpy broadcasting
+ * (shapes right-aligned, size-1 dims broadcast; binary.cpp:59-182).
+ * FLOAT: the op in fp32.  E4M3 / E5M2 (binary.cpp:184-285): both operands
+ * decoded (to half in the reference; every fp8 value is exact there), the
+ * op rounded to half, then the CPU encoder of the same format.
+ */
+ORC_API void orc_fp8_binary(int op, int dtype, const void *a, const int64_t *a_shape, int a_ndim, const void *b,
+                            const int64_t *b_shape, int b_ndim, void *y, const int64_t *y_shape, int y_ndim) {
+    int64_t sa[8], sb[8], n = 1;
+    for (int d = y_ndim - 1, acc_a = 1, acc_b = 1; d >= 0; --d) {
+        int da = d - (y_ndim - a_ndim), db = d - (y_ndim - b_ndim);
+        int64_t ea = da >= 0 ? a_shape[da] : 1, eb = db >= 0 ? b_shape[db] : 1;
+        sa[d] = ea == 1 ? 0 : acc_a;
+        sb[d] = eb == 1 ? 0 : acc_b;
+        acc_a *= (int)ea;
+        acc_b *= (int)eb;
+    }
+    for (int d = 0; d < y_ndim; ++d) n *= y_shape[d];
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t r = i, ia = 0, ib = 0;
+        for (int d = y_ndim - 1; d >= 0; --d) {
+            int64_t c = r % y_shape[d];
+            r /= y_shape[d];
+            ia += c * sa[d];
+            ib += c * sb[d];
+        }
+        float va = dec_any(a, ia, dtype), vb = dec_any(b, ib, dtype);
+        if (dtype == ORC_FLOAT) {
+            float v = op == 0 ? va + vb : op == 1 ? va - vb : op == 2 ? va * vb : va / vb;
+            ((float *)y)[i] = v;
+        } else {
+            double dv = op == 0 ? (double)va + vb : op == 1 ? (double)va - vb : op == 2 ? (double)va * vb
+                                                                            : (double)va / vb;
+            float h = orc_half_round(dv);
+            ((uint8_t *)y)[i] = dtype == ORC_E4M3 ? orc_e4m3_from_float(h) : orc_e5m2_from_float(h);
+        }
+    }
+}
+
+/* QuantizeLinear / DequantizeLinear with a FLOAT8E5M2 tensor. */
+ORC_API void orc_quantize_e5m2(const float *x, uint8_t *y, int64_t outer, int64_t axis_len, int64_t inner,
+                               const float *scale, int saturate) {
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t a = 0; a < axis_len; ++a) {
+            const float s = scale[axis_len == 1 ? 0 : a];
+            for (int64_t i = 0; i < inner; ++i) {
+                const int64_t k = (o * axis_len + a) * inner + i;
+                float q = x[k] / s;
+                if (saturate && !isnan(q) && fabsf(q) > 57344.0f) q = q < 0 ? -57344.0f : 57344.0f;
+                y[k] = orc_e5m2_from_float(q);
+            }
+        }
+}
+
+ORC_API void orc_dequantize_e5m2(const uint8_t *q, float *y, int64_t outer, int64_t axis_len, int64_t inner,
+                                 const float *scale) {
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t a = 0; a < axis_len; ++a) {
+            const float s = scale[axis_len == 1 ? 0 : a];
+            for (int64_t i = 0; i < inner; ++i) {
+                const int64_t k = (o * axis_len + a) * inner + i;
+                y[k] = orc_e5m2_to_float(q[k]) * s;
+            }
         }
 }

@@ -91,3 +91,30 @@ def test_other_entry_point_validation():
                                  0x1000, 1, 64, None) == capi.ERR_INVALID_ARG
     assert L.lcml_fp8_gemm(0, 64, 128, None, 128, None, None, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
                            0x1000, 1, 64, 0, None) == capi.OK  # M == 0: nothing to do
+
+
+def test_fp8_data_type_entry_point_validation():
+    L = capi.lib()
+    sh = lambda t: (ctypes.c_int64 * max(1, len(t)))(*t)
+    F, E4, E5 = capi.DTYPE_FLOAT, capi.DTYPE_FLOAT8E4M3FN, capi.DTYPE_FLOAT8E5M2
+    assert L.lcml_fp8_cast(0x1000, 16, 0x1000, F, 4, None) == capi.ERR_UNSUPPORTED  # bf16 is not an fp8 type
+    assert L.lcml_fp8_cast(0x1000, E4, 0x1000, 99, 4, None) == capi.ERR_UNSUPPORTED
+    assert L.lcml_fp8_cast(None, E4, None, E5, 0, None) == capi.OK  # empty: no-op
+    assert L.lcml_fp8_cast(0x1000, E4, None, E5, 4, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_quantize_e5m2(0x1000, 0x1000, 1, 1, 4, 0x1000, 2, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_quantize_e5m2(0x1000, 0x1000, 1, 0, 4, 0x1000, 1, None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_dequantize_e5m2(0x1000, None, 1, 1, 4, 0x1000, None) == capi.ERR_INVALID_ARG
+    # broadcasting: (2,3) with (4,) does not broadcast; y must be the broadcast shape
+    assert L.lcml_fp8_binary(0, F, 0x1000, sh((2, 3)), 2, 0x1000, sh((4,)), 1, 0x1000, sh((2, 3)), 2,
+                             None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_binary(0, E4, 0x1000, sh((2, 3)), 2, 0x1000, sh((3,)), 1, 0x1000, sh((2, 4)), 2,
+                             None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_binary(7, E4, 0x1000, sh((3,)), 1, 0x1000, sh((3,)), 1, 0x1000, sh((3,)), 1,
+                             None) == capi.ERR_INVALID_ARG
+    assert L.lcml_fp8_binary(0, 16, 0x1000, sh((3,)), 1, 0x1000, sh((3,)), 1, 0x1000, sh((3,)), 1,
+                             None) == capi.ERR_UNSUPPORTED
+    nine = sh((1,) * 9)
+    assert L.lcml_fp8_binary(0, E5, 0x1000, nine, 9, 0x1000, nine, 9, 0x1000, nine, 9,
+                             None) == capi.ERR_INVALID_ARG  # at most 8 dimensions
+    assert L.lcml_fp8_binary(0, E5, None, sh((0, 3)), 2, None, sh((3,)), 1, None, sh((0, 3)), 2,
+                             None) == capi.OK  # empty output: no-op
