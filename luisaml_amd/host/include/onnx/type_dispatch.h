@@ -14,8 +14,11 @@
 namespace lcml::onnx {
 
 // Element types of the FP8 linear path.  The fp8 and bf16 structs are type
-// tags over dense device bytes (one byte per E4M3 element, two per bf16).
+// tags over dense device bytes (one byte per fp8 element, two per bf16).
 struct FP8E4M3FN {
+    uint8_t bits;
+};
+struct FP8E5M2 {
     uint8_t bits;
 };
 struct BFloat16 {
@@ -26,6 +29,7 @@ template <typename T>
 struct TypeName;
 template <> struct TypeName<float> { static constexpr std::string_view value = "float"; };
 template <> struct TypeName<FP8E4M3FN> { static constexpr std::string_view value = "FP8E4M3FN"; };
+template <> struct TypeName<FP8E5M2> { static constexpr std::string_view value = "FP8E5M2"; };
 template <> struct TypeName<BFloat16> { static constexpr std::string_view value = "bfloat16"; };
 template <> struct TypeName<int64_t> { static constexpr std::string_view value = "int64"; };
 template <typename T>
@@ -51,7 +55,7 @@ constexpr TypeIndex type_index_of() noexcept {
 
 }  // namespace refl
 
-using NNTypeList = std::tuple<float, FP8E4M3FN, BFloat16, int64_t>;
+using NNTypeList = std::tuple<float, FP8E4M3FN, FP8E5M2, BFloat16, int64_t>;
 
 namespace detail {
 template <typename Tuple, size_t I = 0, typename F>

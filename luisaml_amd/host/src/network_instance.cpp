@@ -78,7 +78,7 @@ void NetworkInstance::create_tensor_for_var(const Variable &var) {
                         name.c_str());
             auto [start, end] = var.get_buffer_range();
             LCML_ASSERT(end <= weight_bytes_, "variable %s: data_offsets beyond the weight buffer", name.c_str());
-            if constexpr (std::is_same_v<T, FP8E4M3FN>) {
+            if constexpr (std::is_same_v<T, FP8E4M3FN> || std::is_same_v<T, FP8E5M2>) {
                 // FP8 blobs are 4-byte padded (network_instance.cpp:222-224)
                 LCML_ASSERT(end - start == ((n + 3) / 4) * 4, "Weight buffer size mismatch for variable: %s",
                             name.c_str());

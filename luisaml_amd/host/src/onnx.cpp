@@ -67,6 +67,7 @@ refl::TypeIndex data_type_to_type_index(DataType dt) {
     switch (dt) {
     case DataType::FLOAT: return refl::type_index_of<float>();
     case DataType::FLOAT8E4M3FN: return refl::type_index_of<FP8E4M3FN>();
+    case DataType::FLOAT8E5M2: return refl::type_index_of<FP8E5M2>();
     case DataType::BFLOAT16: return refl::type_index_of<BFloat16>();
     case DataType::INT64: return refl::type_index_of<int64_t>();
     default: LCML_ASSERT(false, "Unsupported ONNX DataType on the FP8 path: %s", data_type_name(dt).data());

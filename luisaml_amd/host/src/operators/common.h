@@ -48,12 +48,26 @@ inline AxisView axis_view(const ITensor &t, int axis, size_t nscale) {
 // The optional zero-point input of Q/DQ: ONNX requires 0 for float8 types.
 // A constant zero point is verified; a runtime one (DynamicQuantizeLinear's
 // output) is zero by that operator's definition.
-inline void check_zero_point(std::span<std::reference_wrapper<ITensor>> inputs, size_t idx, const char *op) {
+// The zero point's type is the quantised type (ONNX): it must match `q`.
+inline void check_zero_point(std::span<std::reference_wrapper<ITensor>> inputs, size_t idx, const ITensor &q,
+                             const char *op) {
     if (inputs.size() <= idx) return;
     ITensor &zp = inputs[idx];
-    LCML_ASSERT(is_type<FP8E4M3FN>(zp), "%s: the zero point must be FLOAT8E4M3FN", op);
-    if (auto *c = dynamic_cast<ConstTensor<FP8E4M3FN> *>(&zp))
-        for (uint8_t b : c->const_data()) LCML_ASSERT(b == 0, "%s: float8 zero point must be 0", op);
+    LCML_ASSERT(zp.element_type_index() == q.element_type_index(), "%s: the zero point type must be the fp8 type",
+                op);
+    const std::vector<uint8_t> *bytes = nullptr;
+    if (auto *c = dynamic_cast<ConstTensor<FP8E4M3FN> *>(&zp)) bytes = &c->const_data();
+    if (auto *c = dynamic_cast<ConstTensor<FP8E5M2> *>(&zp)) bytes = &c->const_data();
+    if (bytes)
+        for (uint8_t b : *bytes) LCML_ASSERT(b == 0, "%s: float8 zero point must be 0", op);
+}
+
+// ONNX element type of a float / fp8 tensor for the C ABI (0 if neither)
+inline int fp8_path_dtype(const ITensor &t) {
+    if (is_type<float>(t)) return LCML_DTYPE_FLOAT;
+    if (is_type<FP8E4M3FN>(t)) return LCML_DTYPE_FLOAT8E4M3FN;
+    if (is_type<FP8E5M2>(t)) return LCML_DTYPE_FLOAT8E5M2;
+    return 0;
 }
 
 inline int out_dtype_code(const ITensor &y, const char *op) {

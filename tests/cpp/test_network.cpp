@@ -12,7 +12,11 @@
 //   6. error behaviour (dtype mismatch on bind, FP8 blob size rule);
 //   7. DynamicQuantizeLinear -> DQ -> Conv(DQ(W), B) -> Relu, fused into
 //      FP8Conv and op by op, against the oracle's direct conv;
-//   8. an fp32 grouped / strided / dilated Conv.
+//   8. an fp32 grouped / strided / dilated Conv;
+//   9. E5M2 QuantizeLinear (saturate 1 and 0) / DequantizeLinear, Cast chains
+//      FLOAT -> E5M2 -> E4M3 -> FLOAT, an E5M2 weight blob (4-byte padding);
+//  10. Add / Sub / Mul / Div on FLOAT, E4M3 and E5M2 tensors with
+//      broadcasting, and a DynamicQuantizeLinear zero-point output.
 //   usage: test_network <tests/golden dir>
 #include <cmath>
 #include <cstdio>
@@ -41,6 +45,12 @@ void orc_conv2d(const float *, const float *, const float *, float *, int64_t, i
                 int);
 void orc_gemm_abs_bound(int64_t, int64_t, int64_t, const float *, int, const float *, int, float, float,
                         const float *, int, int64_t, int64_t, double *);
+uint8_t orc_e5m2_from_float(float);
+float orc_e5m2_to_float(uint8_t);
+void orc_quantize_e5m2(const float *, uint8_t *, int64_t, int64_t, int64_t, const float *, int);
+void orc_dequantize_e5m2(const uint8_t *, float *, int64_t, int64_t, int64_t, const float *);
+void orc_fp8_binary(int, int, const void *, const int64_t *, int, const void *, const int64_t *, int, void *,
+                    const int64_t *, int);
 }
 
 static int failures = 0;
@@ -126,7 +136,7 @@ static const Variable &var(Graph &g, const std::string &n, DataType dt, std::vec
 }
 static const Variable &blob_var(Graph &g, Blob &b, const std::string &n, DataType dt, std::vector<size_t> shape,
                                 const void *data, size_t bytes) {
-    size_t padded = dt == DataType::FLOAT8E4M3FN ? (bytes + 3) / 4 * 4 : bytes;
+    size_t padded = dt == DataType::FLOAT8E4M3FN || dt == DataType::FLOAT8E5M2 ? (bytes + 3) / 4 * 4 : bytes;
     auto [s, e] = b.add(data, bytes, padded);
     return g.add_variable(Variable(n, dt, std::move(shape), {}, s, e));
 }
@@ -574,6 +584,168 @@ static void test_errors() {
     CHECK(throws([&] { net.forward(); }));  // Weight buffer size mismatch
 }
 
+static bool same_f32(float a, float b) { return std::isnan(b) ? std::isnan(a) : std::memcmp(&a, &b, 4) == 0; }
+
+static void test_e5m2_qdq_cast() {
+    std::printf("[9] E5M2 QuantizeLinear / DequantizeLinear, Cast chains, E5M2 weight blob (bit-exact)\n");
+    const int R = 6, C = 37;
+    auto x = normals(91, (size_t)R * C, 3000.0f);
+    x[3] = INFINITY;
+    x[4] = -INFINITY;
+    x[5] = NAN;
+    x[6] = -0.0f;
+    x[7] = 2e5f;
+    std::vector<float> s(C);
+    for (int c = 0; c < C; ++c) s[c] = 0.5f + 0.01f * c;
+    std::vector<uint8_t> w(7);  // an E5M2 constant of 7 elements in the blob: padded to 8 bytes
+    for (int i = 0; i < 7; ++i) w[i] = (uint8_t)(0x30 + 5 * i);
+    Blob blob;
+    Graph g("e5");
+    var(g, "x", DataType::FLOAT, {(size_t)R, (size_t)C});
+    raw_var(g, "s", DataType::FLOAT, {(size_t)C}, s.data(), C * 4);
+    var(g, "q1", DataType::FLOAT8E5M2, {(size_t)R, (size_t)C});
+    var(g, "q0", DataType::FLOAT8E5M2, {(size_t)R, (size_t)C});
+    var(g, "d1", DataType::FLOAT, {(size_t)R, (size_t)C});
+    var(g, "c5", DataType::FLOAT8E5M2, {(size_t)R, (size_t)C});
+    var(g, "c4", DataType::FLOAT8E4M3FN, {(size_t)R, (size_t)C});
+    var(g, "cf", DataType::FLOAT, {(size_t)R, (size_t)C});
+    blob_var(g, blob, "w", DataType::FLOAT8E5M2, {7}, w.data(), 7);
+    var(g, "wf", DataType::FLOAT, {7});
+    node(g, "QuantizeLinear", {"x", "s"}, {"q1"}, {Attribute{"axis", (int32_t)1}});
+    node(g, "QuantizeLinear", {"x", "s"}, {"q0"}, {Attribute{"axis", (int32_t)1}, Attribute{"saturate", (int32_t)0}});
+    node(g, "DequantizeLinear", {"q1", "s"}, {"d1"}, {Attribute{"axis", (int32_t)1}});
+    node(g, "Cast", {"x"}, {"c5"}, {Attribute{"to", (int32_t)19}});
+    node(g, "Cast", {"c5"}, {"c4"}, {Attribute{"to", (int32_t)17}});
+    node(g, "Cast", {"c4"}, {"cf"}, {Attribute{"to", (int32_t)1}});
+    node(g, "Cast", {"w"}, {"wf"}, {Attribute{"to", (int32_t)1}});
+    g.add_input("x");
+    for (const char *o : {"q1", "q0", "d1", "cf", "wf"}) g.add_output(o);
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    DeviceBuffer wb(blob.bytes.size());
+    CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+    auto xt = upload(x, {(uint32_t)R, (uint32_t)C});
+    auto q1t = make_device_tensor<FP8E5M2>({(uint32_t)R, (uint32_t)C});
+    auto q0t = make_device_tensor<FP8E5M2>({(uint32_t)R, (uint32_t)C});
+    auto d1t = make_device_tensor<float>({(uint32_t)R, (uint32_t)C});
+    auto cft = make_device_tensor<float>({(uint32_t)R, (uint32_t)C});
+    auto wft = make_device_tensor<float>({7});
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_weight_buffer(static_cast<uint8_t *>(wb.data()), blob.bytes.size());
+    net.set_input("x", *xt);
+    net.set_output("q1", *q1t);
+    net.set_output("q0", *q0t);
+    net.set_output("d1", *d1t);
+    net.set_output("cf", *cft);
+    net.set_output("wf", *wft);
+    net.forward();
+    auto q1 = download<FP8E5M2>(*q1t), q0 = download<FP8E5M2>(*q0t);
+    auto d1 = download<float>(*d1t), cf = download<float>(*cft), wf = download<float>(*wft);
+    std::vector<uint8_t> r1(x.size()), r0(x.size());
+    std::vector<float> rd(x.size());
+    orc_quantize_e5m2(x.data(), r1.data(), R, C, 1, s.data(), 1);
+    orc_quantize_e5m2(x.data(), r0.data(), R, C, 1, s.data(), 0);
+    orc_dequantize_e5m2(r1.data(), rd.data(), R, C, 1, s.data());
+    size_t bad = 0;
+    for (size_t i = 0; i < x.size(); ++i) {
+        bad += q1[i].bits != r1[i];
+        bad += q0[i].bits != r0[i];
+        bad += !same_f32(d1[i], rd[i]);
+        bad += !same_f32(cf[i], orc_e4m3_to_float(orc_e4m3_from_float(orc_e5m2_to_float(orc_e5m2_from_float(x[i])))));
+    }
+    for (int i = 0; i < 7; ++i) bad += !same_f32(wf[i], orc_e5m2_to_float(w[i]));
+    CHECK(bad == 0);
+    CHECK(q0[3].bits == 0x7c && q1[3].bits == 0x7b);  // inf: kept by saturate=0, clamped by saturate=1
+}
+
+static void test_elementwise() {
+    std::printf("[10] Add / Sub / Mul / Div on FLOAT, E4M3, E5M2 with broadcasting; DQL zero point\n");
+    const char *ops[4] = {"Add", "Sub", "Mul", "Div"};
+    uint64_t seed = 1;
+    size_t bad = 0;
+    for (int op = 0; op < 4; ++op) {
+        for (DataType dt : {DataType::FLOAT, DataType::FLOAT8E4M3FN, DataType::FLOAT8E5M2}) {
+            // a [3, 4, 5] with b [4, 1]: y [3, 4, 5]
+            const std::vector<int64_t> sa = {3, 4, 5}, sb = {4, 1}, sy = {3, 4, 5};
+            Graph g("ew");
+            var(g, "a", dt, {3, 4, 5});
+            var(g, "b", dt, {4, 1});
+            var(g, "y", dt, {3, 4, 5});
+            node(g, ops[op], {"a", "b"}, {"y"});
+            g.add_input("a");
+            g.add_input("b");
+            g.add_output("y");
+            Model m(10, "test", "1");
+            m.set_graph(std::move(g));
+            NetworkInstance net;
+            net.set_model(std::move(m));
+            const int code = (int)dt;
+            if (dt == DataType::FLOAT) {
+                auto a = normals(seed++, 60, 1.0f), b = normals(seed++, 4, 1.0f);
+                b[1] = 0.0f;
+                auto at = upload(a, {3, 4, 5});
+                auto bt = upload(b, {4, 1});
+                auto yt = make_device_tensor<float>({3, 4, 5});
+                net.set_input("a", *at);
+                net.set_input("b", *bt);
+                net.set_output("y", *yt);
+                net.forward();
+                auto y = download<float>(*yt);
+                std::vector<float> r(60);
+                orc_fp8_binary(op, code, a.data(), sa.data(), 3, b.data(), sb.data(), 2, r.data(), sy.data(), 3);
+                for (int i = 0; i < 60; ++i) bad += !same_f32(y[i], r[i]);
+            } else {
+                std::vector<uint8_t> a(60), b(4);
+                for (int i = 0; i < 60; ++i) a[i] = (uint8_t)((i * 37 + op * 11 + seed) & 0xff);
+                for (int i = 0; i < 4; ++i) b[i] = (uint8_t)((i * 101 + 7 * op) & 0xff);
+                ++seed;
+                auto run = [&]<typename T>() {
+                    std::vector<T> ah(60), bh(4);
+                    for (int i = 0; i < 60; ++i) ah[i].bits = a[i];
+                    for (int i = 0; i < 4; ++i) bh[i].bits = b[i];
+                    auto at = upload(ah, {3, 4, 5});
+                    auto bt = upload(bh, {4, 1});
+                    auto yt = make_device_tensor<T>({3, 4, 5});
+                    net.set_input("a", *at);
+                    net.set_input("b", *bt);
+                    net.set_output("y", *yt);
+                    net.forward();
+                    auto y = download<T>(*yt);
+                    std::vector<uint8_t> r(60);
+                    orc_fp8_binary(op, code, a.data(), sa.data(), 3, b.data(), sb.data(), 2, r.data(), sy.data(), 3);
+                    for (int i = 0; i < 60; ++i) bad += y[i].bits != r[i];
+                };
+                if (dt == DataType::FLOAT8E4M3FN) run.template operator()<FP8E4M3FN>();
+                else run.template operator()<FP8E5M2>();
+            }
+        }
+    }
+    CHECK(bad == 0);
+    // DynamicQuantizeLinear's y_zero_point output is written as 0
+    Graph g("dq");
+    var(g, "x", DataType::FLOAT, {2, 8});
+    var(g, "y", DataType::FLOAT8E4M3FN, {2, 8});
+    var(g, "s", DataType::FLOAT, {1});
+    var(g, "z", DataType::FLOAT8E4M3FN, {1});
+    node(g, "DynamicQuantizeLinear", {"x"}, {"y", "s", "z"});
+    g.add_input("x");
+    g.add_output("z");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    auto xt = upload(normals(77, 16, 1.0f), {2, 8});
+    auto zt = make_device_tensor<FP8E4M3FN>({1});
+    std::vector<FP8E4M3FN> junk(1);
+    junk[0].bits = 0x55;
+    CHECK(hipMemcpy(zt->device_data(), junk.data(), 1, hipMemcpyHostToDevice) == hipSuccess);
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_input("x", *xt);
+    net.set_output("z", *zt);
+    net.forward();
+    CHECK(download<FP8E4M3FN>(*zt)[0].bits == 0);
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -592,6 +764,8 @@ int main(int argc, char **argv) {
         test_qdq_conv(false);
         test_qdq_conv(true, 2);
         test_f32_grouped_conv();
+        test_e5m2_qdq_cast();
+        test_elementwise();
         test_errors();
     } catch (const Error &e) {
         std::printf("FAIL: uncaught error: %s\n", e.what());
