@@ -12,8 +12,11 @@
 // (no tracing); prepare() runs once and (1) fuses DequantizeLinear(W_fp8) ->
 // Gemm/MatMul [-> Relu/Gelu], with QuantizeLinear/DynamicQuantizeLinear ->
 // DequantizeLinear on the activation, into one FP8Linear node, and (2) packs
-// every fused FP8 weight into MFMA panels once, at load time.
+// every fused FP8 weight into MFMA panels once, at load time, and (3) plans
+// one device arena for the intermediates by live range (memory_planner.h).
 #pragma once
+
+#include <unordered_map>
 
 #include <hip/hip_runtime.h>
 
@@ -21,6 +24,7 @@
 #include <string>
 #include <vector>
 
+#include "onnx/memory_planner.h"
 #include "onnx/onnx.h"
 #include "onnx/tensor_table.h"
 
@@ -49,6 +53,9 @@ public:
 };
 
 class NetworkInstance {
+    // declared before the tensor table: the planned intermediates are views
+    // into it (they also share its ownership)
+    std::shared_ptr<DeviceBuffer> arena_;
     Model model_;
     TensorTable table_;
     std::vector<std::unique_ptr<Operator>> ops_;
@@ -57,7 +64,10 @@ class NetworkInstance {
     const uint8_t *weight_buffer_ = nullptr;  // device
     size_t weight_bytes_ = 0;
     bool fusion_ = true;
+    bool memory_planning_ = true;
     bool prepared_ = false;
+    MemoryPlan plan_;
+    std::unordered_map<std::string, size_t> planned_;  // intermediate -> arena offset
     size_t fused_count_ = 0;
     std::vector<std::pair<std::string, std::reference_wrapper<ITensor>>> inputs_, outputs_;
 
@@ -65,6 +75,7 @@ class NetworkInstance {
     void validate_and_bind(std::string_view role, const Variable &var, ITensor &t);
     void fuse_qdq_linear();
     void pack_weights();
+    void plan_intermediates();
 
 public:
     NetworkInstance() = default;
@@ -81,6 +92,11 @@ public:
     void set_output(std::string_view name, ITensor &t);
     // QDQ -> FP8Linear fusion (default on); off runs every node as written.
     void set_fusion(bool on) { fusion_ = on; }
+    // Intermediates share one arena by live range (default on); off gives
+    // every intermediate its own allocation.
+    void set_memory_planning(bool on) { memory_planning_ = on; }
+    const MemoryPlan &memory_plan() const { return plan_; }
+    size_t planned_intermediates() const { return planned_.size(); }
     // The reference's warp-width knob (network_instance.h:50-54); a gfx950
     // wavefront is 64 lanes and the kernels choose their own launch shapes.
     uint32_t warp_size() const { return 64; }

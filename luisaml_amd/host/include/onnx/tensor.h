@@ -71,6 +71,11 @@ public:
     // borrow memory owned elsewhere
     DeviceArray(void *base, size_t byte_offset, size_t count, bool is_view = false)
         : base_(base), byte_offset_(byte_offset), count_(count), view_(is_view) {}
+    // a region of a shared buffer (the planned arena of intermediates)
+    DeviceArray(std::shared_ptr<DeviceBuffer> owner, size_t byte_offset, size_t count)
+        : owner_(std::move(owner)), byte_offset_(byte_offset), count_(count), view_(true) {
+        base_ = owner_->data();
+    }
     // view of another array's storage
     DeviceArray(const DeviceArray &src, size_t elem_offset, size_t count)
         : owner_(src.owner_), base_(src.base_), byte_offset_(src.byte_offset_ + elem_offset * elem_bytes),

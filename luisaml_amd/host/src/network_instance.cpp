@@ -103,6 +103,8 @@ void NetworkInstance::create_tensor_for_var(const Variable &var) {
             hip_check(hipMemcpy(arr.data(), raw.data(), raw.size(), hipMemcpyHostToDevice), "hipMemcpy");
             table_.own(name, std::make_unique<ConstTensor<T>>(shape, std::move(arr),
                                                               std::vector<uint8_t>(raw.begin(), raw.end())));
+        } else if (auto it = planned_.find(name); it != planned_.end()) {
+            table_.own(name, std::make_unique<NNTensor<T>>(shape, DeviceArray<T>(arena_, it->second, n)));
         } else {
             LCML_ASSERT(!shape.empty() || n == 1, "variable %s has no static shape", name.c_str());
             table_.own(name, make_device_tensor<T>(shape));
@@ -374,6 +376,43 @@ void NetworkInstance::pack_weights() {
     }
 }
 
+// Intermediates (written by a node, not bound from outside, not constants)
+// share one arena: each is live from its producer through its last reader
+// in node order, and the planner lets disjoint live ranges share bytes.
+void NetworkInstance::plan_intermediates() {
+    planned_.clear();
+    arena_.reset();
+    plan_ = MemoryPlan{};
+    if (!memory_planning_) return;
+    const auto &nodes = model_.get_graph().get_nodes();
+    std::unordered_map<std::string, size_t> index;
+    std::vector<BufferRequest> reqs;
+    std::vector<std::string> names;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        for (auto &in : nodes[i].get_inputs()) {
+            auto it = index.find(in.get().get_name());
+            if (it != index.end()) reqs[it->second].last = std::max(reqs[it->second].last, i);
+        }
+        for (auto &out : nodes[i].get_outputs()) {
+            const Variable &v = out.get();
+            if (table_.contains(v.get_name()) || v.is_trainable_weight() || !v.get_raw_data().empty()) continue;
+            if (v.get_shape().empty() && v.num_elements() != 1) continue;  // no static shape: allocated on its own
+            auto [it, fresh] = index.try_emplace(v.get_name(), reqs.size());
+            if (fresh) {
+                reqs.push_back({v.num_elements() * data_type_bytes(v.get_dtype()), i, i});
+                names.push_back(v.get_name());
+            } else {
+                reqs[it->second].last = std::max(reqs[it->second].last, i);
+            }
+        }
+    }
+    if (reqs.empty()) return;
+    plan_ = plan_device_buffers(reqs);
+    LCML_ASSERT(plan_is_valid(reqs, plan_), "memory plan: overlapping live buffers");
+    arena_ = std::make_shared<DeviceBuffer>(plan_.arena_bytes);
+    for (size_t r = 0; r < reqs.size(); ++r) planned_[names[r]] = plan_.offsets[r];
+}
+
 void NetworkInstance::prepare() {
     Graph &g = model_.mutable_graph();
     g.mark_constants();
@@ -383,6 +422,7 @@ void NetworkInstance::prepare() {
     for (auto &[name, t] : inputs_) validate_and_bind("input", g.get_var(name), t.get());
     for (auto &[name, t] : outputs_) validate_and_bind("output", g.get_var(name), t.get());
     pack_weights();
+    plan_intermediates();
     for (const Node &n : g.get_nodes()) {
         for (auto &v : n.get_inputs()) create_tensor_for_var(v.get());
         for (auto &v : n.get_outputs()) create_tensor_for_var(v.get());

@@ -16,7 +16,9 @@
 //   9. E5M2 QuantizeLinear (saturate 1 and 0) / DequantizeLinear, Cast chains
 //      FLOAT -> E5M2 -> E4M3 -> FLOAT, an E5M2 weight blob (4-byte padding);
 //  10. Add / Sub / Mul / Div on FLOAT, E4M3 and E5M2 tensors with
-//      broadcasting, and a DynamicQuantizeLinear zero-point output.
+//      broadcasting, and a DynamicQuantizeLinear zero-point output;
+//  11. the device-buffer planner: a 9-node graph run with one planned arena
+//      and with one allocation per intermediate, bit-identical outputs.
 //   usage: test_network <tests/golden dir>
 #include <cmath>
 #include <cstdio>
@@ -746,6 +748,62 @@ static void test_elementwise() {
     CHECK(download<FP8E4M3FN>(*zt)[0].bits == 0);
 }
 
+static void test_memory_planner() {
+    std::printf("[11] intermediates in one planned arena vs one allocation each\n");
+    const uint32_t R = 64, C = 1024;
+    auto build = []() {
+        Graph g("plan");
+        const std::vector<size_t> sh = {64, 1024};
+        var(g, "x", DataType::FLOAT, sh);
+        float s = 0.05f;
+        raw_var(g, "s", DataType::FLOAT, {1}, &s, 4);
+        for (const char *n : {"a", "b", "d", "e", "f", "h", "y"}) var(g, n, DataType::FLOAT, sh);
+        var(g, "q", DataType::FLOAT8E4M3FN, sh);
+        var(g, "q5", DataType::FLOAT8E5M2, sh);
+        node(g, "Add", {"x", "x"}, {"a"});
+        node(g, "Mul", {"a", "x"}, {"b"});
+        node(g, "QuantizeLinear", {"b", "s"}, {"q"});
+        node(g, "DequantizeLinear", {"q", "s"}, {"d"});
+        node(g, "Sub", {"d", "x"}, {"e"});
+        node(g, "Relu", {"e"}, {"f"});
+        node(g, "QuantizeLinear", {"f", "s"}, {"q5"});
+        node(g, "DequantizeLinear", {"q5", "s"}, {"h"});
+        node(g, "Add", {"h", "a"}, {"y"});  // a stays live across the whole graph
+        g.add_input("x");
+        g.add_output("y");
+        Model m(10, "test", "1");
+        m.set_graph(std::move(g));
+        return m;
+    };
+    auto xt = upload(normals(111, (size_t)R * C, 1.0f), {R, C});
+    std::vector<float> y[2];
+    size_t arena = 0, unshared = 0, planned = 0;
+    for (int mode = 0; mode < 2; ++mode) {
+        auto yt = make_device_tensor<float>({R, C});
+        NetworkInstance net;
+        net.set_model(build());
+        net.set_memory_planning(mode == 0);
+        net.set_input("x", *xt);
+        net.set_output("y", *yt);
+        net.forward();
+        net.forward();  // a second pass over the same arena
+        y[mode] = download<float>(*yt);
+        if (mode == 0) {
+            arena = net.memory_plan().arena_bytes;
+            unshared = net.memory_plan().unshared_bytes;
+            planned = net.planned_intermediates();
+        } else {
+            CHECK(net.planned_intermediates() == 0);
+        }
+    }
+    CHECK(planned == 8);
+    CHECK(std::memcmp(y[0].data(), y[1].data(), y[0].size() * 4) == 0);
+    // a is live throughout; the others chain: three fp32 slots (a plus two
+    // alternating) hold every fp32 intermediate, the fp8 ones fit beside them
+    std::printf("    arena %zu bytes for %zu bytes of intermediates\n", arena, unshared);
+    CHECK(arena < unshared && arena <= (size_t)3 * R * C * 4 + (size_t)R * C);
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -766,6 +824,7 @@ int main(int argc, char **argv) {
         test_f32_grouped_conv();
         test_e5m2_qdq_cast();
         test_elementwise();
+        test_memory_planner();
         test_errors();
     } catch (const Error &e) {
         std::printf("FAIL: uncaught error: %s\n", e.what());

@@ -3,12 +3,14 @@
 // JSON import of the reference's own MLP fixture, operator creation from
 // the imported nodes, the tensor API and the error behaviour.
 //   usage: test_registry <tests/golden dir>
+#include <algorithm>
 #include <cstdio>
 #include <fstream>
 #include <sstream>
 #include <string>
 #include <cstring>
 
+#include "onnx/memory_planner.h"
 #include "onnx/network_instance.h"
 #include "onnx/onnx.h"
 #include "onnx/tensor.h"
@@ -50,8 +52,46 @@ int main(int argc, char **argv) {
     auto &opset = OperatorSet::get_default();
     CHECK(opset.get_domain() == "default" && opset.get_version() == 21);
     for (const char *op : {"Gemm", "MatMul", "QuantizeLinear", "DequantizeLinear", "DynamicQuantizeLinear", "Cast",
-                           "Relu", "Gelu", "FP8Linear"})
+                           "Relu", "Gelu", "FP8Linear", "Conv", "FP8Conv", "Add", "Sub", "Mul", "Div"})
         CHECK(opset.has_operator(op));
+
+    // ---- device-buffer planner (host only) ----
+    {
+        // a chain: buffer i written by node i, read by node i+1 -> two slots
+        std::vector<BufferRequest> chain;
+        for (size_t i = 0; i < 6; ++i) chain.push_back({1000, i, i + 1});
+        MemoryPlan p = plan_device_buffers(chain);
+        CHECK(plan_is_valid(chain, p) && p.arena_bytes == 2 * 1024 && p.unshared_bytes == 6 * 1024);
+        // all live at once -> no sharing
+        std::vector<BufferRequest> all = {{300, 0, 5}, {5000, 1, 4}, {17, 2, 3}, {4096, 0, 3}};
+        p = plan_device_buffers(all);
+        CHECK(plan_is_valid(all, p) && p.arena_bytes == p.unshared_bytes);
+        // a small buffer fits the gap a large one left
+        std::vector<BufferRequest> gap = {{4096, 0, 1}, {4096, 2, 3}, {1024, 1, 2}, {8192, 0, 3}};
+        p = plan_device_buffers(gap);
+        CHECK(plan_is_valid(gap, p) && p.arena_bytes == 8192 + 4096 + 1024);
+        // random graphs: always valid, never larger than no sharing, never
+        // smaller than the peak of simultaneously live bytes
+        uint64_t st = 12345;
+        auto rnd = [&](uint64_t m) { st = st * 6364136223846793005ull + 1442695040888963407ull; return (st >> 33) % m; };
+        for (int t = 0; t < 200; ++t) {
+            std::vector<BufferRequest> r;
+            const size_t nodes = 2 + rnd(30);
+            for (size_t k = 0, nb = 1 + rnd(40); k < nb; ++k) {
+                size_t a = rnd(nodes), b = a + rnd(nodes - a);
+                r.push_back({1 + rnd(1 << 20), a, b});
+            }
+            p = plan_device_buffers(r);
+            size_t peak = 0;
+            for (size_t nd = 0; nd < nodes; ++nd) {
+                size_t live = 0;
+                for (auto &q : r)
+                    if (q.first <= nd && nd <= q.last) live += (q.bytes + 255) / 256 * 256;
+                peak = std::max(peak, live);
+            }
+            CHECK(plan_is_valid(r, p) && p.arena_bytes <= p.unshared_bytes && p.arena_bytes >= peak);
+        }
+    }
     CHECK(!opset.has_operator("NotAnOp"));
     Node bogus("n", "NotAnOp");
     CHECK(throws([&] { opset.create_operator("NotAnOp", bogus); }));
