@@ -159,6 +159,14 @@ def main() -> int:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)
 
+    def warm(fn, ms: float = 40.0):
+        """Untimed repeats of fn for about `ms` of GPU time, so the sub-benchmarks
+        below are timed at steady clocks rather than on the ramp."""
+        t = timed(fn)
+        for _ in range(max(1, min(200, int(ms / max(t, 1e-3))))):
+            fn()
+        torch.cuda.synchronize()
+
     # eager warmup, then the timed region: one replay of a graph holding
     # exactly `steps` steps (launch gaps of the Python/ctypes caller removed)
     for i in range(args.warmup):
@@ -277,7 +285,7 @@ def main() -> int:
                          ("quantize_dynamic", lambda: capi.quantize_dynamic(a, out=q_out, scale_out=s_q,
                                                                             workspace=ws_q)),
                          ("dequantize", lambda: capi.dequantize(qa, sa, out=b))):
-            fn()
+            warm(fn)
             n = max(5, args.steps)
             ms = timed(lambda: [fn() for _ in range(n)]) / n
             gbs = 5.0 * nq / (ms * 1e-3) / 1e9
@@ -292,8 +300,7 @@ def main() -> int:
         big = {}
         for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
                                  ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
-            for _ in range(max(1, args.warmup // 2)):
-                capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern)
+            warm(lambda: capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern))
             n = max(3, args.steps // 2)
             ms = timed(lambda: [capi.gemm(qa, sa, bp, sb, BIG, BIG, out=y, kernel=kern) for _ in range(n)]) / n
             tflops = 2.0 * BIG ** 3 / (ms * 1e-3) / 1e12
@@ -361,7 +368,7 @@ def main() -> int:
         blk = {}
         for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
                                  ("native_fp8_mfma", capi.KERNEL_MFMA_FP8, FP8_PEAK_TFLOPS)):
-            block(kern)
+            warm(lambda: block(kern))
             n = max(2, args.steps // 4)
             ms = timed(lambda: [block(kern) for _ in range(n)]) / n
             tf = flops_block / (ms * 1e-3) / 1e12
@@ -399,7 +406,7 @@ def main() -> int:
         def quant_c():
             capi.quantize_nhwc(xc, out=xq, scale_out=sxc, workspace=wsq)
 
-        quant_c()
+        warm(quant_c)
         n = max(3, args.steps // 2)
         q_ms = timed(lambda: [quant_c() for _ in range(n)]) / n
         for name, kern, peak in (("exact_bf16_mfma", capi.KERNEL_MFMA, BF16_PEAK_TFLOPS),
@@ -407,7 +414,7 @@ def main() -> int:
             def conv_c():
                 capi.conv2d(xq, sxc, bpc, d_wsc, cco, (3, 3), pads=(1, 1), bias=bc, act=capi.ACT_RELU, out=yc,
                             kernel=kern)
-            conv_c()
+            warm(conv_c)
             ms = timed(lambda: [conv_c() for _ in range(n)]) / n
             tf = conv_flops / (ms * 1e-3) / 1e12
             conv[name] = {"conv_ms": round(ms, 4), "tflops": round(tf, 1),

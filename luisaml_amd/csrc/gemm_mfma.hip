@@ -449,13 +449,10 @@ using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
 template <bool EXACT, bool CONV>
 hipError_t launch(GemmArgs &g, hipStream_t s) {
     auto *fn = k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, EXACT, CONV>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, Shipped::LDS_BYTES);
-        if (err != hipSuccess) return err;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (hipError_t err = ensure_dynamic_lds(reinterpret_cast<const void *>(fn), Shipped::LDS_BYTES, lds_set);
+        err != hipSuccess)
+        return err;
     int64_t Kp = pad_to(g.K, kPackK), Np = pad_to(g.N, kPanelCols);
     g.KC = Kp / 16;
     g.npanels = Np / 64;

@@ -371,12 +371,8 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
     const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
     const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, true, true>)
                            : reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, false, true>);
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[exact]) {
-        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kSkinnyDynLdsMax);
-        if (err != hipSuccess) return err;
-        attr_set[exact] = true;
-    }
+    static std::atomic<uint64_t> lds_set[2];
+    if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess) return err;
     if (exact)
         hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true, true>), dim3(grid), dim3(W * 64), lds, s, g);
     else

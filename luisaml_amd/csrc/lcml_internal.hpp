@@ -7,6 +7,8 @@
 
 #include "lcml_device.hpp"
 
+#include <atomic>
+
 namespace lcml {
 
 hipError_t launch_quantize(const float *x, uint8_t *y, int64_t outer, int64_t axis_len,
@@ -85,5 +87,20 @@ struct BcastGeom {
 };
 hipError_t launch_fp8_binary(int op, int fmt, const void *a, const void *b, void *y, int64_t n, bool same_shape,
                              const BcastGeom &g, hipStream_t s);
+
+// A kernel's dynamic-LDS limit (hipFuncSetAttribute) is per device: set it
+// once per (kernel, device), tracked in `done` (bit d = device d; devices past
+// 63 set it on every call).  The call is idempotent, so two threads racing on
+// the first launch both succeed.
+inline hipError_t ensure_dynamic_lds(const void *fn, int bytes, std::atomic<uint64_t> &done) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return err;
+}
 
 }  // namespace lcml
