@@ -145,3 +145,46 @@ def test_argument_errors(dev):
     rc = capi.lib().lcml_fp8_binary(0, F, a.data_ptr(), sh((2, 3)), 2, b.data_ptr(), sh((4,)), 1, a.data_ptr(),
                                     sh((2, 3)), 2, None)
     assert rc == capi.ERR_INVALID_ARG
+
+
+def test_scalar_paths_unaligned_and_ragged(dev):
+    """Pointers that are not 16-byte aligned and axis views with inner % 4 != 0
+    take the element-wise code paths; results stay bit-exact."""
+    rng = np.random.default_rng(42)
+    x = (rng.normal(size=4099) * 100).astype(np.float32)
+    xd = to_dev(np.concatenate([[0.0], x]).astype(np.float32), dev)[1:]  # 4-byte aligned, not 16
+    assert xd.data_ptr() % 16 != 0
+    got = capi.cast(xd, F, E5).cpu().numpy()
+    assert np.array_equal(got, oracle.e5m2_from_float(x))
+    codes = rng.integers(0, 256, 4099, dtype=np.uint8)
+    cd = to_dev(np.concatenate([[0], codes]).astype(np.uint8), dev)[1:]  # odd address
+    assert f32_equal(capi.cast(cd, E5, F).cpu().numpy(), oracle.e5m2_decode_table()[codes])
+    # per-axis E5M2 with inner = 3 (no groups of four share a scale)
+    xs = (rng.normal(size=(5, 7, 3)) * 50).astype(np.float32)
+    s = (rng.random(7) + 0.1).astype(np.float32)
+    q = capi.quantize_e5m2(to_dev(xs, dev), to_dev(s, dev), axis=1).cpu().numpy()
+    assert np.array_equal(q, oracle.quantize_e5m2(xs, s, axis=1))
+    assert f32_equal(capi.dequantize_e5m2(to_dev(q, dev), to_dev(s, dev), axis=1).cpu().numpy(),
+                     oracle.dequantize_e5m2(q, s, axis=1))
+
+
+def test_binary_eight_dims_and_unaligned_fp32(dev):
+    rng = np.random.default_rng(8)
+    sa, sb = (2, 1, 3, 1, 2, 1, 2, 3), (1, 2, 1, 2, 1, 3, 1, 1)
+    for dtype in (F, E4, E5):
+        if dtype == F:
+            a = rng.normal(size=sa).astype(np.float32)
+            b = rng.normal(size=sb).astype(np.float32)
+        else:
+            a = rng.integers(0, 256, size=sa, dtype=np.uint8)
+            b = rng.integers(0, 256, size=sb, dtype=np.uint8)
+        got = capi.binary(capi.BINARY_MUL, to_dev(a, dev), to_dev(b, dev), dtype).cpu().numpy()
+        ref = oracle.fp8_binary(capi.BINARY_MUL, dtype, a, b)
+        assert (f32_equal(got, ref) if dtype == F else np.array_equal(got, ref)), dtype
+    # same-shape fp32 operands at 4-byte (not 16-byte) alignment: element path
+    a = rng.normal(size=1031).astype(np.float32)
+    b = rng.normal(size=1031).astype(np.float32)
+    ad = to_dev(np.concatenate([[0.0], a]).astype(np.float32), dev)[1:]
+    bd = to_dev(np.concatenate([[0.0], b]).astype(np.float32), dev)[1:]
+    got = capi.binary(capi.BINARY_DIV, ad, bd, F).cpu().numpy()
+    assert f32_equal(got, oracle.fp8_binary(capi.BINARY_DIV, F, a, b))
