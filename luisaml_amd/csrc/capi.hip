@@ -147,6 +147,27 @@ int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is
                       "lcml_fp8_unpack_weight");
 }
 
+namespace {
+// AUTO's choice between the 256x256-tile MFMA kernel and the skinny kernel
+// (64 columns x 16*mb rows per workgroup, one workgroup per CU).  Both
+// times grow linearly in K; measured on K = 4096 and 11008, a 256x256 tile
+// takes 4.3-5.2x as long as a skinny workgroup with mb = 4 (0.7x that with
+// mb = 2, 0.55x with mb = 1), and each kernel runs in waves of 256
+// workgroups.  While the MFMA grid leaves CUs idle (fewer than 256 tiles,
+// so one wave of 4.5 units), the skinny kernel wins up to about 1150
+// workgroups: 4096x11008 at M = 384 (85 us against 94 us), not at M = 512
+// (101 against 93).
+int auto_gemm_kernel(int64_t M, int64_t N) {
+    if (M <= 16) return LCML_KERNEL_SKINNY;
+    const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
+    if (tiles >= 256) return LCML_KERNEL_MFMA;
+    const int64_t rows = M <= 32 ? 32 : 64;
+    const double wgs = (double)((N + 63) / 64) * (double)((M + rows - 1) / rows);
+    const double skinny = (wgs > 256 ? wgs / 256 : 1.0) * (rows == 32 ? 0.7 : 1.0);
+    return skinny < 4.5 ? LCML_KERNEL_SKINNY : LCML_KERNEL_MFMA;
+}
+}  // namespace
+
 int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda, const float *a_scale,
                   const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
                   const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
@@ -165,7 +186,7 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
         return fail(LCML_ERR_INVALID_ARG, "%s: a must be 16-byte aligned with lda >= K, lda %% 16 == 0", fn);
     if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
     hipStream_t s = (hipStream_t)stream;
-    if (kernel == LCML_KERNEL_AUTO) kernel = M <= 16 ? LCML_KERNEL_SKINNY : LCML_KERNEL_MFMA;
+    if (kernel == LCML_KERNEL_AUTO) kernel = auto_gemm_kernel(M, N);
     hipError_t err;
     switch (kernel) {
     case LCML_KERNEL_MFMA:
@@ -177,10 +198,12 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
         break;
     case LCML_KERNEL_SKINNY:
     case LCML_KERNEL_SKINNY_FP8:
-        if (M > 16) return fail(LCML_ERR_UNSUPPORTED, "%s: the skinny kernel takes M <= 16 (M=%lld)", fn, (long long)M);
         // buffer extents are 32-bit: the activations and one weight panel
         if ((M - 1) * lda + K >= (int64_t)0x80000000 || lcml::pad_to(K, lcml::kPackK) * 64 >= (int64_t)0x80000000)
             return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the skinny kernel", fn);
+        if ((M + 63) / 64 * ((N + 63) / 64) >= (int64_t)0x80000000)
+            return fail(LCML_ERR_UNSUPPORTED, "%s: M=%lld N=%lld exceeds the skinny kernel's grid", fn, (long long)M,
+                        (long long)N);
         err = lcml::launch_gemm_skinny(M, N, K, a, lda, b_packed, e, kernel == LCML_KERNEL_SKINNY, s);
         break;
     case LCML_KERNEL_VALU: err = lcml::launch_gemv_valu_fp8(M, N, K, a, lda, b_packed, e, s); break;

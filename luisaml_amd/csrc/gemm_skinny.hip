@@ -1,4 +1,5 @@
-// gemm_skinny.hip -- small-M (decode-shaped, M <= 16) FP8 GEMM on gfx950.
+// gemm_skinny.hip -- small- and medium-M FP8 GEMM on gfx950 (decode-shaped
+// M <= 16, and any M whose 256x256-tile grid would leave CUs idle).
 //
 // The weight matrix is read exactly once, straight from HBM into registers
 // as 128-bit loads in packed-panel order (no LDS staging: every weight byte
@@ -9,6 +10,10 @@
 // partial 16x16 tiles are summed through LDS before the epilogue.  The
 // activations (M <= 16 rows, padded to 16 with zeros) are re-read from L2 by
 // every workgroup, 16*K bytes each, so NB also sets that re-read traffic.
+// Larger M: a workgroup takes MB = 2 or 4 row blocks of 16 (each weight
+// fragment, converted once, feeds MB MFMAs), and M > 64 adds row groups of
+// 64 rows, i.e. more workgroups per weight panel; those are numbered so
+// that the row groups of one panel run on one XCD and share its L2.
 // The activation rows are the A operand: lane l holds row l%16,
 // k = (l/16)*32+0..31 of each 128-k block; the weight operand: lane l holds
 // column l%16 of a 16-column block and the same k range, i.e. two
@@ -68,6 +73,7 @@ struct SkinnyArgs {
     int64_t KC;      // k-chunks per panel
     int64_t nblk16;  // 16-column blocks in the packed matrix (Np / 16)
     int nkb;         // K blocks of 128
+    int rg;          // row groups of 16*MB rows (workgroups per column range)
     Epilogue e;
 };
 
@@ -80,15 +86,27 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-template <int NB, int WAVES, int UNROLL, bool EXACT, bool DYN>
+template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
+    static_assert(!DYN || MB == 1, "the fused quantiser serves M <= 16");
     constexpr int NT = WAVES * 64;
     __shared__ v4f red[WAVES][NB][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // DYN: [M][pitch] E4M3
     // the wavefront index is uniform: readfirstlane lets the compiler keep
     // everything derived from it (the K range, the in-range tests) scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t blk0 = (int64_t)blockIdx.x * NB;  // first 16-column block
+    // Workgroup -> (column range, row group).  With several row groups the
+    // workgroups that read one weight panel should share an L2: workgroup
+    // ids go round-robin over the 8 XCDs (id % 8), so ids are regrouped into
+    // one contiguous range per XCD, in which the row groups of a panel are
+    // consecutive.
+    int64_t t = blockIdx.x;
+    if (g.rg > 1) {
+        const int64_t nwg = (int64_t)gridDim.x, q = nwg >> 3, r = nwg & 7, x = t & 7;
+        t = x * q + (x < r ? x : r) + (t >> 3);
+    }
+    const int64_t blk0 = (t / g.rg) * NB;                   // first 16-column block
+    const int64_t row0 = (t - (t / g.rg) * g.rg) * 16 * MB;  // first row
 
     // K range of this wavefront
     const int kb_begin = (int)(((int64_t)g.nkb * wave) / WAVES);
@@ -101,8 +119,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // compiler's vmcnt waits count exactly the loads issued after it (a load
     // under a branch makes it wait for every outstanding load instead, which
     // would drain the weight prefetch at each use).
-    const int arow = lane & 15;
-    const bool a_ok = arow < g.M;
+    const int arow = lane & 15;  // row within a 16-row block
+    bool a_ok[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) a_ok[mb] = row0 + mb * 16 + arow < g.M;
 
     // weights: this workgroup's 64-column panel (NB 16-column blocks)
     const int64_t panel0 = blk0 >> 2;
@@ -117,14 +137,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // activations (E4M3, without DYN): row lane%16, k offset (lane/16)*32 of a K block
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, DYN ? 0 : (int)((g.M - 1) * g.lda + g.K), kRsrcFlags);
-    const uint32_t a_row_off = (uint32_t)(arow * g.lda) + (uint32_t)(lane >> 4) * 32;
-
-    v4f acc[NB];
+    uint32_t a_row_off[MB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < MB; ++mb)
+        a_row_off[mb] = (uint32_t)((row0 + mb * 16 + arow) * g.lda) + (uint32_t)(lane >> 4) * 32;
+
+    v4f acc[MB][NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[mb][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     struct Frag {
-        u4 alo[UNROLL], ahi[UNROLL], blo[UNROLL][NB], bhi[UNROLL][NB];
+        u4 alo[UNROLL][MB], ahi[UNROLL][MB], blo[UNROLL][NB], bhi[UNROLL][NB];
     };
     auto load = [&](Frag &f, int kb0) {
 #pragma unroll
@@ -139,12 +164,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
             }
             if constexpr (!DYN) {
                 const uint32_t k = (uint32_t)kb * 128 + (uint32_t)(lane >> 4) * 32;  // K < 2^31
-                const uint32_t o = a_row_off + (uint32_t)kb * 128;
-                const bool ok = in & a_ok;
-                const uint32_t o_lo = (ok & (k < (uint32_t)g.K)) ? o : kOOB;
-                const uint32_t o_hi = (ok & (k + 16 < (uint32_t)g.K)) ? o + 16 : kOOB;
-                f.alo[u] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_lo, 0, 0);
-                f.ahi[u] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_hi, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const uint32_t o = a_row_off[mb] + (uint32_t)kb * 128;
+                    const bool ok = in & a_ok[mb];
+                    const uint32_t o_lo = (ok & (k < (uint32_t)g.K)) ? o : kOOB;
+                    const uint32_t o_hi = (ok & (k + 16 < (uint32_t)g.K)) ? o + 16 : kOOB;
+                    f.alo[u][mb] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_lo, 0, 0);
+                    f.ahi[u][mb] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_hi, 0, 0);
+                }
             }
         }
     };
@@ -154,10 +182,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const int kb = kb0 + u;
-            const uint8_t *p = a_lds + (a_ok ? arow : 0) * pitch + (int64_t)kb * 128 + (lane >> 4) * 32;
-            const bool ok = a_ok && kb < kb_end;
-            f.alo[u] = ok ? *reinterpret_cast<const u4 *>(p) : u4{0, 0, 0, 0};
-            f.ahi[u] = ok ? *reinterpret_cast<const u4 *>(p + 16) : u4{0, 0, 0, 0};
+            const uint8_t *p = a_lds + (a_ok[0] ? arow : 0) * pitch + (int64_t)kb * 128 + (lane >> 4) * 32;
+            const bool ok = a_ok[0] && kb < kb_end;
+            f.alo[u][0] = ok ? *reinterpret_cast<const u4 *>(p) : u4{0, 0, 0, 0};
+            f.ahi[u][0] = ok ? *reinterpret_cast<const u4 *>(p + 16) : u4{0, 0, 0, 0};
         }
     };
     // blocks past the wavefront's range hold zeros and are skipped (a
@@ -167,25 +195,41 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         for (int u = 0; u < UNROLL; ++u) {
             if (kb0 + u >= kb_end) continue;
             if constexpr (EXACT) {
-                const uint32_t aw[8] = {f.alo[u].x, f.alo[u].y, f.alo[u].z, f.alo[u].w,
-                                        f.ahi[u].x, f.ahi[u].y, f.ahi[u].z, f.ahi[u].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const bf16x8 a16 = e4m3x8_to_bf16(aw[2 * q], aw[2 * q + 1]);
+                    bf16x8 a16[MB];
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        const u4 lo = f.alo[u][mb], hi = f.ahi[u][mb];
+                        a16[mb] = q == 0 ? e4m3x8_to_bf16(lo.x, lo.y)
+                                : q == 1 ? e4m3x8_to_bf16(lo.z, lo.w)
+                                : q == 2 ? e4m3x8_to_bf16(hi.x, hi.y)
+                                         : e4m3x8_to_bf16(hi.z, hi.w);
+                    }
 #pragma unroll
                     for (int j = 0; j < NB; ++j) {
-                        const uint32_t bw[8] = {f.blo[u][j].x, f.blo[u][j].y, f.blo[u][j].z, f.blo[u][j].w,
-                                                f.bhi[u][j].x, f.bhi[u][j].y, f.bhi[u][j].z, f.bhi[u][j].w};
-                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            a16, e4m3x8_to_bf16(bw[2 * q], bw[2 * q + 1]), acc[j], 0, 0, 0);
+                        const u4 lo = f.blo[u][j], hi = f.bhi[u][j];
+                        const bf16x8 b16 = q == 0 ? e4m3x8_to_bf16(lo.x, lo.y)
+                                         : q == 1 ? e4m3x8_to_bf16(lo.z, lo.w)
+                                         : q == 2 ? e4m3x8_to_bf16(hi.x, hi.y)
+                                                  : e4m3x8_to_bf16(hi.z, hi.w);
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb)
+                            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a16[mb], b16, acc[mb][j], 0, 0, 0);
                     }
                 }
             } else {
-                v8i af = join(f.alo[u], f.ahi[u]);
+                v8i af[MB];
 #pragma unroll
-                for (int j = 0; j < NB; ++j)
-                    acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        af, join(f.blo[u][j], f.bhi[u][j]), acc[j], 0, 0, 0, 0, 0, 0);
+                for (int mb = 0; mb < MB; ++mb) af[mb] = join(f.alo[u][mb], f.ahi[u][mb]);
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const v8i bf = join(f.blo[u][j], f.bhi[u][j]);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+                        acc[mb][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mb], bf, acc[mb][j], 0, 0,
+                                                                                     0, 0, 0, 0);
+                }
             }
         }
     };
@@ -312,23 +356,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         }
     }
 
-#pragma unroll
-    for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[j];
-    __syncthreads();
-
-    // 16 x 16*NB outputs: (block j, lane l, register r); MFMA output layout:
-    // lane l holds column l%16 and rows (l/16)*4 + r.
+    // 16 x 16*NB outputs per row block: (block j, lane l, register r); MFMA
+    // output layout: lane l holds column l%16 and rows (l/16)*4 + r.  Row
+    // blocks go through the one LDS reduction buffer in turn.
     const Epilogue &e = g.e;
     const float a_s = DYN ? a_dyn : (e.a_scale ? e.a_scale[0] : 1.0f);
-    for (int o = tid; o < NB * 256; o += NT) {
-        const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
-        const int64_t row = (l >> 4) * 4 + r;
-        const int64_t col = (blk0 + j) * 16 + (l & 15);
-        if (row >= e.M || col >= e.N) continue;
-        float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
-        epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
+    for (int mb = 0; mb < MB; ++mb) {
+        if (mb) __syncthreads();  // the previous block's sums are read
+#pragma unroll
+        for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[mb][j];
+        __syncthreads();
+        for (int o = tid; o < NB * 256; o += NT) {
+            const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
+            const int64_t row = row0 + mb * 16 + (l >> 4) * 4 + r;
+            const int64_t col = (blk0 + j) * 16 + (l & 15);
+            if (row >= e.M || col >= e.N) continue;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
+            epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
+        }
     }
 }
 
@@ -345,11 +393,24 @@ hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a,
     g.e = e;
     g.x = nullptr; g.ldx = 0; g.scale_out = nullptr;
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
-    unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
-    if (exact)
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true, false>), dim3(grid), dim3(W * 64), 0, s, g);
-    else
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, false, false>), dim3(grid), dim3(W * 64), 0, s, g);
+    // row blocks of 16 per workgroup (every weight fragment feeds MB MFMAs),
+    // and row groups of 64 beyond that
+    const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    g.rg = (int)((M + 16 * mb - 1) / (16 * mb));
+    const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB * g.rg);
+#define LCML_SKINNY_LAUNCH(MBV)                                                                                  \
+    if (exact)                                                                                                 \
+        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, true, false>), dim3(grid), dim3(W * 64), 0, s, g);     \
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, false, false>), dim3(grid), dim3(W * 64), 0, s, g)
+    if (mb == 1) {
+        LCML_SKINNY_LAUNCH(1);
+    } else if (mb == 2) {
+        LCML_SKINNY_LAUNCH(2);
+    } else {
+        LCML_SKINNY_LAUNCH(4);
+    }
+#undef LCML_SKINNY_LAUNCH
     return hipGetLastError();
 }
 
@@ -365,18 +426,19 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
     g.KC = Kp / 16;
     g.nblk16 = Np / 16;
     g.nkb = (int)(Kp / 128);
+    g.rg = 1;
     g.e = e;
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
     const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
-    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, true, true>)
-                           : reinterpret_cast<const void *>(k_gemm_skinny<NB, W, U, false, true>);
+    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true>)
+                           : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true>);
     static std::atomic<uint64_t> lds_set[2];
     if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess) return err;
     if (exact)
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, true, true>), dim3(grid), dim3(W * 64), lds, s, g);
+        hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true>), dim3(grid), dim3(W * 64), lds, s, g);
     else
-        hipLaunchKernelGGL((k_gemm_skinny<NB, W, U, false, true>), dim3(grid), dim3(W * 64), lds, s, g);
+        hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true>), dim3(grid), dim3(W * 64), lds, s, g);
     return hipGetLastError();
 }
 

@@ -68,7 +68,7 @@ def _gemm(**kw):
     (dict(lda=100), capi.ERR_INVALID_ARG),
     (dict(a=0x1001), capi.ERR_INVALID_ARG),
     (dict(kernel=99), capi.ERR_INVALID_ARG),
-    (dict(M=17, kernel=capi.KERNEL_SKINNY), capi.ERR_UNSUPPORTED),
+    (dict(M=1 << 20, K=4096, lda=4096, kernel=capi.KERNEL_SKINNY), capi.ERR_UNSUPPORTED),  # > 2 GiB of A
     (dict(c=0x1000, c_ndim=1, c0=7), capi.ERR_INVALID_ARG),
     (dict(c=0x1000, c_ndim=2, c0=3, c1=64), capi.ERR_INVALID_ARG),
 ])
