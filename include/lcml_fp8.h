@@ -154,7 +154,7 @@ LCML_API int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N,
  *    even), row pitch ldy elements.
  * kernel: LCML_KERNEL_* (AUTO picks SKINNY for M <= 16; for larger M it
  *    picks SKINNY while the 256x256 MFMA grid has fewer than 256 tiles and
- *    the skinny grid at most about 1150 workgroups, else MFMA).
+ *    a measured cost model of the two kernels favours it, else MFMA).
  * Replaces the per-thread fma loop nest of Gemm::apply (gemm.cpp:27-325) and
  * MatMul (src/onnx/operators/mat_mul.cpp:51-186) for the DQ->Gemm pattern.
  */

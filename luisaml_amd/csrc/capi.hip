@@ -148,22 +148,19 @@ int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is
 }
 
 namespace {
-// AUTO's choice between the 256x256-tile MFMA kernel and the skinny kernel
-// (64 columns x 16*mb rows per workgroup, one workgroup per CU).  Both
-// times grow linearly in K; measured on K = 4096 and 11008, a 256x256 tile
-// takes 4.3-5.2x as long as a skinny workgroup with mb = 4 (0.7x that with
-// mb = 2, 0.55x with mb = 1), and each kernel runs in waves of 256
-// workgroups.  While the MFMA grid leaves CUs idle (fewer than 256 tiles,
-// so one wave of 4.5 units), the skinny kernel wins up to about 1150
-// workgroups: 4096x11008 at M = 384 (85 us against 94 us), not at M = 512
-// (101 against 93).
-int auto_gemm_kernel(int64_t M, int64_t N) {
+// AUTO's choice between the 256x256-tile MFMA kernel and the skinny kernel.
+// Both times grow about linearly in K.  While the MFMA grid leaves CUs idle
+// (fewer than 256 tiles) it runs one round of tiles, and a 256x256 tile
+// takes 4.3-5.2x as long as a skinny workgroup with 4 row blocks (measured
+// on K = 4096 and 11008); the skinny kernel's time in those units comes
+// from lcml::skinny_row_blocks.  At M = 384: 4096x11008 skinny 71 us
+// against 93 us, 11008x4096 70 us against 205 us.
+int auto_gemm_kernel(int64_t M, int64_t N, int64_t K) {
     if (M <= 16) return LCML_KERNEL_SKINNY;
     const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
     if (tiles >= 256) return LCML_KERNEL_MFMA;
-    const int64_t rows = M <= 32 ? 32 : 64;
-    const double wgs = (double)((N + 63) / 64) * (double)((M + rows - 1) / rows);
-    const double skinny = (wgs > 256 ? wgs / 256 : 1.0) * (rows == 32 ? 0.7 : 1.0);
+    double skinny = 0;
+    lcml::skinny_row_blocks(M, N, K, &skinny);
     return skinny < 4.5 ? LCML_KERNEL_SKINNY : LCML_KERNEL_MFMA;
 }
 }  // namespace
@@ -186,7 +183,7 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
         return fail(LCML_ERR_INVALID_ARG, "%s: a must be 16-byte aligned with lda >= K, lda %% 16 == 0", fn);
     if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
     hipStream_t s = (hipStream_t)stream;
-    if (kernel == LCML_KERNEL_AUTO) kernel = auto_gemm_kernel(M, N);
+    if (kernel == LCML_KERNEL_AUTO) kernel = auto_gemm_kernel(M, N, K);
     hipError_t err;
     switch (kernel) {
     case LCML_KERNEL_MFMA:

@@ -11,9 +11,9 @@
 // activations (M <= 16 rows, padded to 16 with zeros) are re-read from L2 by
 // every workgroup, 16*K bytes each, so NB also sets that re-read traffic.
 // Larger M: a workgroup takes MB = 2 or 4 row blocks of 16 (each weight
-// fragment, converted once, feeds MB MFMAs), and M > 64 adds row groups of
-// 64 rows, i.e. more workgroups per weight panel; those are numbered so
-// that the row groups of one panel run on one XCD and share its L2.
+// fragment, converted once, feeds MB MFMAs), and M > 16*MB adds row groups
+// of 16*MB rows, i.e. more workgroups per weight panel; those are numbered
+// so that the row groups of one panel run on one XCD and share its L2.
 // The activation rows are the A operand: lane l holds row l%16,
 // k = (l/16)*32+0..31 of each 128-k block; the weight operand: lane l holds
 // column l%16 of a 16-column block and the same k range, i.e. two
@@ -36,6 +36,8 @@
 // M=1, +2.8 us at M=2, +5 us at M=4 over the GEMM alone, against about
 // +4.5 us for the separate quantise launch), so the fused kernel only pays
 // off for small M*K.
+#include <algorithm>
+
 #include "lcml_internal.hpp"
 
 namespace lcml {
@@ -386,6 +388,38 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 
 }  // namespace
 
+// Row blocks per workgroup.  A workgroup with MB = 4 holds 152-164 VGPRs,
+// so one runs per CU; with MB = 2 (99-119 VGPRs) two share a CU.  Measured
+// on the 4096x11008 and 11008x4096 linears, in units of one MB = 4
+// workgroup's time T (19 us at K = 4096, 38 us at K = 11008): r rounds of
+// up to 256 MB = 4 workgroups take 0.2 + 0.8 r; MB = 2 workgroups, n per CU
+// at most, take 0.33 + 0.38 n.  So MB = 2 wins where it fills CUs that
+// MB = 4 leaves idle (11008x4096 at M = 128: 26 us against 37 us), MB = 4
+// where both fill the chip (4096x11008 at M = 64: 19 us against 22 us).
+// With two MB = 2 workgroups per CU, the weight panels resident on one XCD
+// at a time must also fit its 4 MB L2, or the row groups of a panel re-read
+// it from memory (28672x8192 at M = 128: 16 panels of 512 KB per XCD, 133 us
+// against 114 us with MB = 4): then MB = 4.
+int skinny_row_blocks(int64_t M, int64_t N, int64_t K, double *cost) {
+    const int64_t panels = (N + 63) / 64;
+    auto rounds = [&](int64_t rows) { return (double)((panels * ((M + rows - 1) / rows) + 255) / 256); };
+    int mb;
+    double c;
+    if (M <= 16) {
+        mb = 1;
+        c = 0.55 * rounds(16);
+    } else {
+        const double n = rounds(32), c2 = 0.33 + 0.38 * n, c4 = 0.2 + 0.8 * rounds(64);
+        const double rg2 = (double)((M + 31) / 32);
+        const double per_xcd = std::min((double)panels * rg2, 512.0) / 8;  // resident MB = 2 workgroups
+        const bool l2_fits = per_xcd / rg2 * (double)pad_to(K, kPackK) * 64 <= 4.0 * 1024 * 1024;
+        mb = M <= 32 || (c2 <= c4 && (n < 2 || l2_fits)) ? 2 : 4;
+        c = mb == 2 ? c2 : c4;
+    }
+    if (cost) *cost = c;
+    return mb;
+}
+
 hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                               const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
     SkinnyArgs g;
@@ -398,8 +432,8 @@ hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a,
     g.x = nullptr; g.ldx = 0; g.scale_out = nullptr;
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
     // row blocks of 16 per workgroup (every weight fragment feeds MB MFMAs),
-    // and row groups of 64 beyond that
-    const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    // and row groups of 16*MB rows beyond that
+    const int mb = skinny_row_blocks(M, N, K, nullptr);
     g.rg = (int)((M + 16 * mb - 1) / (16 * mb));
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB * g.rg);
 #define LCML_SKINNY_LAUNCH(MBV)                                                                                  \

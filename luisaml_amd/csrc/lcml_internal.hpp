@@ -52,6 +52,9 @@ hipError_t launch_pack_conv_weight(const uint8_t *w, int Cout, int Cin_g, int KH
                                    hipStream_t s);
 hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                               const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
+// the skinny kernel's 16-row blocks per workgroup (1, 2 or 4) for an M x N
+// output over K, and its modelled time in units of one 4-block workgroup's run
+int skinny_row_blocks(int64_t M, int64_t N, int64_t K, double *cost);
 // fused DynamicQuantizeLinear + skinny GEMM (fp32 activations, M <= 16):
 // LDS use is skinny_dynamic_lds_bytes(M, K) <= kSkinnyDynLdsMax
 constexpr int64_t kSkinnyDynLdsMax = 128 * 1024 - 32 * 1024;

@@ -53,6 +53,18 @@ def test_medium_m_shapes(dev, M, N, K):
     assert_close(y, ref, bound)
 
 
+@pytest.mark.parametrize("M,N,K", [(48, 11008, 256), (100, 16384, 128), (128, 16384, 128), (65, 11008, 256),
+                                   (200, 11008, 128)])
+def test_medium_m_row_block_choices(dev, M, N, K):
+    """Wide outputs, where the kernel's cost model takes 4 row blocks per
+    workgroup (M=48 on 172 panels; M=100 and 128 on 256 panels, two row
+    groups) or 2 with several row groups (M=65, M=200)."""
+    c = make_case(M, N, K, seed=M + 3, dev=dev)
+    y = run(c, capi.KERNEL_SKINNY, dev=dev).cpu().numpy()
+    ref, bound = reference(c)
+    assert_close(y, ref, bound)
+
+
 @pytest.mark.parametrize("M", [24, 64, 150])
 def test_medium_m_epilogue(dev, M):
     """Row-dependent bias [M, N] and an activation through the row groups."""
