@@ -30,6 +30,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP8_PEAK_TFLOPS = 5000.0       # dense FP8 MFMA
 BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA (the exact kernel's instruction)
 SMALL_K, SMALL_N, SMALL_MS = 4096, 11008, (1, 4, 16)
+MEDIUM_MS = (32, 64, 128, 256)  # the same linear past decode sizes (a sub-benchmark, not the value)
 BIG = 8192
 N_WEIGHT_COPIES = 7
 
@@ -263,6 +264,30 @@ def main() -> int:
         lib_ref["small_m_fp8_scaled_mm_us"] = fp8_us
         lib_ref["small_m_fp8_scaled_mm_gbs"] = {m: round(gemm_kernel_bytes(int(m)) / (t * 1e-6) / 1e9, 1)
                                                 for m, t in fp8_us.items()}
+        # medium M on the same linear: AUTO (the skinny kernel with 2 or 4
+        # row blocks per workgroup here) against the 256x256-tile kernel and
+        # the library, E4M3 activations in, bf16 out
+        med = {}
+        for M in MEDIUM_MS:
+            qx = capi.quantize(torch.from_numpy(synth.normal(400 + M, (M, K))).to(dev), one)
+            x8 = qx.view(torch.float8_e4m3fn)
+            yv = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            row = {}
+            for name, kern in (("auto_us", capi.KERNEL_AUTO), ("tile_kernel_us", capi.KERNEL_MFMA)):
+                gm = capture(lambda i, kern=kern: capi.gemm(qx, one, packed[i % N_WEIGHT_COPIES], d_sw, N, K,
+                                                             out=yv, kernel=kern), 3 * args.steps)
+                gm.replay()
+                row[name] = round(1e3 * timed(gm.replay) / (3 * args.steps), 2)
+                del gm
+            gl = capture(lambda i: torch._scaled_mm(x8, w8[i % N_WEIGHT_COPIES].t(), scale_a=one, scale_b=one,
+                                                    out_dtype=torch.bfloat16), 3 * args.steps)
+            gl.replay()
+            row["hipblaslt_fp8_us"] = round(1e3 * timed(gl.replay) / (3 * args.steps), 2)
+            del gl
+            row["auto_tflops"] = round(2.0 * M * K * N / (row["auto_us"] * 1e-6) / 1e12, 1)
+            med[str(M)] = row
+        out["medium_m"] = {"workload": f"x[M,{K}] E4M3 x W[{K},{N}] E4M3 (per-channel scales), bf16 out, "
+                                       f"{N_WEIGHT_COPIES} weight copies rotated", **med}
         del w8
     except Exception as exc:  # an older torch without ROCm fp8 GEMM
         lib_ref["small_m_error"] = f"{type(exc).__name__}: {str(exc)[:120]}"
