@@ -384,8 +384,21 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         __syncthreads();
         if constexpr (CONV) {
             // NCHW output: lanes run along output pixels (rows), so each
-            // column's stores are contiguous
+            // column's stores are contiguous.  The column's scale and a
+            // row-invariant bias are read once per block (lane c holds column
+            // c) and taken per column with v_readlane, so the column loop has
+            // no memory reads besides the staged sums and several stores in
+            // flight; a bias that varies over rows is read per element.
             const uint32_t ohw = (uint32_t)(g.cv.OH * g.cv.OW);
+            const int64_t colb = n0 + wn * WN * 32 + j * 32;  // first column of this block
+            const int ncol = colb < e.N ? (int)(e.N - colb < 32 ? e.N - colb : 32) : 0;
+            const bool inv = !e.c || epi_c_row_invariant(e);
+            const int64_t lc = colb + (lane & 31) < e.N ? colb + (lane & 31) : e.N - 1;  // in range
+            int sc_l = __builtin_bit_cast(int, epi_scale(e, a_s, lc));
+            int cv_l = __builtin_bit_cast(int, e.c && inv ? epi_c(e, 0, lc) : 0.0f);
+            // pinned here, where every lane is active: v_readlane below reads
+            // lanes that the row test may have switched off
+            asm volatile("" : "+v"(sc_l), "+v"(cv_l));
 #pragma unroll
             for (int h = 0; h < WM / 2; ++h) {
                 const int rl = h * 64 + lane;
@@ -393,15 +406,29 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 if (m < e.M) {
                     const uint32_t n = (uint32_t)m / ohw, pix = (uint32_t)m - n * ohw;
                     const int64_t ybase = ((int64_t)n * g.cv.CoutTot + (int64_t)grp * e.N) * ohw + pix;
+                    if (inv) {
+#pragma unroll 4
+                        for (int c = 0; c < ncol; ++c) {
+                            const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc_l, c));
+                            const float cv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(cv_l, c));
+                            const float v = epi_value_cv(e, sc, cv, st[rl * EP_PITCH + c]);
+                            const int64_t yi = ybase + (colb + c) * ohw;
+                            if (e.y_bf16)
+                                reinterpret_cast<uint16_t *>(e.y)[yi] = bf16_rne(v);
+                            else
+                                reinterpret_cast<float *>(e.y)[yi] = v;
+                        }
+                    } else {
 #pragma unroll 1
-                    for (int c = 0; c < 32; ++c) {
-                        const int64_t col = n0 + wn * WN * 32 + j * 32 + c;
-                        if (col >= e.N) break;
-                        const float v = epi_value(e, epi_scale(e, a_s, col), m, col, st[rl * EP_PITCH + c]);
-                        if (e.y_bf16)
-                            reinterpret_cast<uint16_t *>(e.y)[ybase + col * ohw] = bf16_rne(v);
-                        else
-                            reinterpret_cast<float *>(e.y)[ybase + col * ohw] = v;
+                        for (int c = 0; c < ncol; ++c) {
+                            const int64_t col = colb + c;
+                            const float v = epi_value(e, __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc_l, c)),
+                                                      m, col, st[rl * EP_PITCH + c]);
+                            if (e.y_bf16)
+                                reinterpret_cast<uint16_t *>(e.y)[ybase + col * ohw] = bf16_rne(v);
+                            else
+                                reinterpret_cast<float *>(e.y)[ybase + col * ohw] = v;
+                        }
                     }
                 }
             }
