@@ -131,6 +131,24 @@ def test_fused_limits_and_errors(dev):
         capi._check(rc)
 
 
+@pytest.mark.parametrize("mag", [1e-25, 1e-3, 3e17, 1e30])
+def test_fused_scale_outside_fast_range(dev, mag):
+    """Activations so small or large that the scale leaves the reciprocal
+    fast path's range: the fused kernel's encode takes the exact-division
+    form and still matches the two-call composition and the oracle."""
+    M, N, K = 6, 192, 400
+    x = (synth.normal(40, (M, K)) * np.float32(mag)).astype(np.float32)
+    qw, sw, bp, d_sw = weights(K, N, 41, dev)
+    x_d = to_dev(x, dev)
+    s_out = torch.empty(1, dtype=torch.float32, device=dev)
+    y = capi.gemm_dynamic(x_d, bp, d_sw, N, K, kernel=capi.KERNEL_SKINNY, scale_out=s_out)
+    y2, q2, s2 = two_step(x_d, bp, d_sw, N, K, capi.KERNEL_SKINNY)
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    assert s_out.cpu().numpy().view(np.uint32)[0] == s_ref.view(np.uint32)
+    assert np.array_equal(q2.cpu().numpy(), oracle.quantize(x, s_ref))
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+
+
 SCALES = [1.0, 0.0137, 1 / 448, 3.3e-3, 0.7, 5.5, 123.25, 2.0 ** -59, 2.0 ** 39, 1e-30, 3e20, 6.1e-5]
 
 
