@@ -300,6 +300,10 @@ void NetworkInstance::fuse_qdq_linear() {
         if (A.get_shape().empty() || A.get_shape().back() != K) continue;
         // ---- A: static QDQ, dynamic QDQ, or fp32 ----
         ActQ aq = match_act(A, i);
+        // E4M3 activation rows need a 16-byte pitch (K % 16 == 0); otherwise
+        // the activation's Q/DQ nodes stay and the fused node runs W8A32 on
+        // their (exactly representable) fp32 output
+        if (aq.a_mode != 0 && K % 16 != 0) aq = ActQ{0, &A, nullptr, {}};
         const int a_mode = aq.a_mode;  // 0: fp32 (W8A32), 1: static scale, 2: dynamic per-tensor
         const Variable *a_src = aq.src, *a_scale = aq.scale;
         std::vector<size_t> drop = {prod_idx(B.get_name())};
