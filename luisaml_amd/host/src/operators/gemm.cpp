@@ -45,6 +45,12 @@ public:
     }
 };
 
+// MatMul with numpy semantics, as the reference (mat_mul.cpp:45-303): a 1-D
+// A is one row and a 1-D B one column (both dropped from Y); batch
+// dimensions are right-aligned and broadcast where they are 1.  A 2-D B
+// (the linear-layer case) is one GEMM over all of A's rows; a batched B is
+// one GEMM per output batch, each a sequential fma chain per output as the
+// reference's own (B rows are not contiguous along k there either).
 class MatMul : public StreamOperator {
 public:
     MatMul() : StreamOperator("MatMul") {}
@@ -53,13 +59,56 @@ public:
         LCML_ASSERT(inputs.size() == 2 && outputs.size() == 1, "MatMul requires 2 inputs and 1 output.");
         ITensor &A = inputs[0], &B = inputs[1], &Y = outputs[0];
         LCML_ASSERT(is_type<float>(A) && is_type<float>(B), "MatMul: unfused operands must be float");
-        LCML_ASSERT(B.ndim() == 2, "MatMul: batched B is outside the FP8 linear path");
-        const int64_t K = A.shape(A.ndim() - 1), N = B.shape(1), M = A.size() / K;
-        LCML_ASSERT(B.shape(0) == K, "MatMul: inner dimensions mismatch");
-        check(lcml_fp8_sgemm(M, N, K, static_cast<const float *>(A.device_data()), K, 0,
-                             static_cast<const float *>(B.device_data()), N, 0, 1.0f, nullptr, 0, 0, 0, 0.0f,
-                             LCML_ACT_NONE, Y.device_data(), out_dtype_code(Y, "MatMul"), N, stream_),
-              "MatMul");
+        const int an = (int)A.ndim(), bn = (int)B.ndim();
+        LCML_ASSERT(an >= 1 && bn >= 1, "MatMul: operands must have at least one dimension");
+        const int64_t K = A.shape(an - 1), M = an >= 2 ? A.shape(an - 2) : 1;
+        const int64_t KB = bn >= 2 ? B.shape(bn - 2) : B.shape(0), N = bn >= 2 ? B.shape(bn - 1) : 1;
+        LCML_ASSERT(KB == K, "MatMul: inner dimensions mismatch (K=%lld vs %lld)", (long long)K, (long long)KB);
+        const int ydt = out_dtype_code(Y, "MatMul");
+        const float *a = static_cast<const float *>(A.device_data());
+        const float *b = static_cast<const float *>(B.device_data());
+        char *y = static_cast<char *>(Y.device_data());
+        const size_t esz = ydt == LCML_DTYPE_BFLOAT16 ? 2 : 4;
+        if (bn <= 2) {  // every row of A against one B
+            const int64_t rows = (int64_t)A.size() / K;
+            LCML_ASSERT((int64_t)Y.size() == rows * N, "MatMul: output has %u elements, expected %lld", Y.size(),
+                        (long long)(rows * N));
+            check(lcml_fp8_sgemm(rows, N, K, a, K, 0, b, N, 0, 1.0f, nullptr, 0, 0, 0, 0.0f, LCML_ACT_NONE, y, ydt,
+                                 N, stream_),
+                  "MatMul");
+            return;
+        }
+        // batch dimensions, right-aligned
+        const int ab = an >= 2 ? an - 2 : 0, bb = bn - 2, nb = ab > bb ? ab : bb;
+        std::vector<int64_t> ydim(nb), astr(nb, 0), bstr(nb, 0);
+        int64_t sa = M * K, sb = K * N;
+        for (int d = nb - 1; d >= 0; --d) {
+            const int ai = d - (nb - ab), bi = d - (nb - bb);
+            const int64_t ad = ai >= 0 ? A.shape(ai) : 1, bd = bi >= 0 ? B.shape(bi) : 1;
+            LCML_ASSERT(ad == bd || ad == 1 || bd == 1, "MatMul: batch dimensions %lld and %lld do not broadcast",
+                        (long long)ad, (long long)bd);
+            ydim[d] = ad > bd ? ad : bd;
+            if (ad > 1) astr[d] = sa;
+            if (bd > 1) bstr[d] = sb;
+            sa *= ad;
+            sb *= bd;
+        }
+        int64_t batches = 1;
+        for (int64_t v : ydim) batches *= v;
+        LCML_ASSERT((int64_t)Y.size() == batches * M * N, "MatMul: output has %u elements, expected %lld", Y.size(),
+                    (long long)(batches * M * N));
+        std::vector<int64_t> idx(nb, 0);
+        for (int64_t t = 0; t < batches; ++t) {
+            int64_t ao = 0, bo = 0;
+            for (int d = 0; d < nb; ++d) {
+                ao += idx[d] * astr[d];
+                bo += idx[d] * bstr[d];
+            }
+            check(lcml_fp8_sgemm(M, N, K, a + ao, K, 0, b + bo, N, 0, 1.0f, nullptr, 0, 0, 0, 0.0f, LCML_ACT_NONE,
+                                 y + (size_t)(t * M * N) * esz, ydt, N, stream_),
+                  "MatMul");
+            for (int d = nb - 1; d >= 0 && ++idx[d] == ydim[d]; --d) idx[d] = 0;
+        }
     }
 };
 

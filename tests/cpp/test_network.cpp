@@ -20,6 +20,7 @@
 //  11. the device-buffer planner: a 9-node graph run with one planned arena
 //      and with one allocation per intermediate, bit-identical outputs.
 //   usage: test_network <tests/golden dir>
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -806,6 +807,81 @@ static void test_memory_planner() {
     CHECK(arena < unshared && arena <= (size_t)3 * R * C * 4 + (size_t)R * C);
 }
 
+// fp32 MatMul with numpy semantics (mat_mul.cpp:187-303): 1-D operands and
+// right-aligned batch dimensions broadcast where they are 1; every output
+// batch against the oracle's GEMM of the matching A and B slices.
+static void test_batched_matmul() {
+    std::printf("[12] fp32 MatMul: batched, broadcast and 1-D operands\n");
+    struct Case {
+        std::vector<size_t> a, b, y;
+    };
+    const Case cases[] = {{{2, 3, 5, 7}, {3, 7, 4}, {2, 3, 5, 4}}, {{5, 8}, {2, 1, 8, 6}, {2, 1, 5, 6}},
+                          {{7}, {3, 7, 4}, {3, 4}},                 {{2, 1, 5, 7}, {1, 3, 7, 4}, {2, 3, 5, 4}},
+                          {{2, 5, 7}, {7}, {2, 5}},                  {{4, 9}, {9, 3}, {4, 3}}};
+    int ci = 0;
+    for (const Case &c : cases) {
+        auto count = [](const std::vector<size_t> &v) {
+            size_t n = 1;
+            for (size_t d : v) n *= d;
+            return n;
+        };
+        auto x = normals(120 + ci, count(c.a), 1.0f), w = normals(130 + ci, count(c.b), 1.0f);
+        ++ci;
+        Graph g("mm");
+        Blob blob;
+        var(g, "a", DataType::FLOAT, c.a);
+        blob_var(g, blob, "B", DataType::FLOAT, c.b, w.data(), w.size() * 4);
+        var(g, "y", DataType::FLOAT, c.y);
+        node(g, "MatMul", {"a", "B"}, {"y"});
+        g.add_input("a");
+        g.add_output("y");
+        Model m(10, "test", "1");
+        m.set_graph(std::move(g));
+        DeviceBuffer wb(blob.bytes.size());
+        CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+        ITensor::shape_type as(c.a.begin(), c.a.end()), ys(c.y.begin(), c.y.end());
+        auto at = upload(x, as);
+        auto yt = make_device_tensor<float>(ys);
+        NetworkInstance net;
+        net.set_model(std::move(m));
+        net.set_weight_buffer(wb.data(), blob.bytes.size());
+        net.set_input("a", *at);
+        net.set_output("y", *yt);
+        net.forward();
+        auto y = download<float>(*yt);
+        // reference: treat 1-D A as [1, K] and 1-D B as [K, 1]; pad batch dims on the left with 1
+        const size_t K = c.a.back(), M = c.a.size() >= 2 ? c.a[c.a.size() - 2] : 1;
+        const size_t N = c.b.size() >= 2 ? c.b.back() : 1;
+        std::vector<size_t> ab(c.a.begin(), c.a.size() >= 2 ? c.a.end() - 2 : c.a.begin());
+        std::vector<size_t> bb(c.b.begin(), c.b.size() >= 2 ? c.b.end() - 2 : c.b.begin());
+        const size_t nb = std::max(ab.size(), bb.size());
+        ab.insert(ab.begin(), nb - ab.size(), 1);
+        bb.insert(bb.begin(), nb - bb.size(), 1);
+        std::vector<size_t> yb(nb);
+        size_t batches = 1;
+        for (size_t d = 0; d < nb; ++d) batches *= (yb[d] = std::max(ab[d], bb[d]));
+        CHECK(y.size() == batches * M * N);
+        std::vector<float> ref(y.size());
+        std::vector<double> bound(y.size());
+        for (size_t t = 0; t < batches; ++t) {
+            size_t rem = t, ai = 0, bi = 0, am = 1, bm = 1;
+            for (size_t d = nb; d-- > 0;) {
+                const size_t coord = rem % yb[d];
+                rem /= yb[d];
+                ai += (ab[d] == 1 ? 0 : coord) * am;
+                bi += (bb[d] == 1 ? 0 : coord) * bm;
+                am *= ab[d];
+                bm *= bb[d];
+            }
+            orc_gemm(M, N, K, x.data() + ai * M * K, 0, w.data() + bi * K * N, 0, 1.0f, 0.0f, nullptr, -1, 0, 0, 0,
+                     ref.data() + t * M * N);
+            orc_gemm_abs_bound(M, N, K, x.data() + ai * M * K, 0, w.data() + bi * K * N, 0, 1.0f, 0.0f, nullptr, -1,
+                               0, 0, bound.data() + t * M * N);
+        }
+        CHECK(close(y, ref, bound, 1e-5, 0.0, "batched matmul"));
+    }
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -826,6 +902,7 @@ int main(int argc, char **argv) {
         test_qdq_conv(false);
         test_qdq_conv(true, 2);
         test_f32_grouped_conv();
+        test_batched_matmul();
         test_e5m2_qdq_cast();
         test_elementwise();
         test_memory_planner();
