@@ -80,8 +80,8 @@ def main() -> int:
                     help="also run one plain 256 MiB device copy (profiler byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only (the kernels run on one GPU's share; there is no "
+              "multi-GPU path); run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch

@@ -348,8 +348,8 @@ void NetworkInstance::fuse_qdq_linear() {
     nodes = std::move(out);
 }
 
-// Load-time packing of every fused weight (north star: weights pre-laid-out
-// at model load into MFMA-fragment order with their fp32 scales).
+// Load-time packing of every fused weight: weights are laid out at model
+// load in MFMA-fragment order, beside their fp32 scales.
 void NetworkInstance::pack_weights() {
     for (const Node &n : model_.get_graph().get_nodes()) {
         const bool conv = n.get_op_type() == "FP8Conv";

@@ -1,6 +1,6 @@
 """ctypes bindings for the CPU oracle (oracle/lcml_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: the oracle is the parity checker and the timed CPU
+TEST INFRASTRUCTURE ONLY: the oracle is what parity is judged against and the timed CPU
 baseline.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
 import this package; the product library (luisaml_amd) never does.
 

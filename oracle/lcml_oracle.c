@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This file restates, on the CPU, the arithmetic
  * of the reference ONNX runtime (LuisaGroup/LuisaML) that the HIP library in
- * luisaml_amd/ replaces.  It is the parity checker and the timed CPU
+ * luisaml_amd/ replaces.  It is what parity is judged against and the timed CPU
  * baseline; it is never linked into, loaded by or called from the product
  * library.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it.

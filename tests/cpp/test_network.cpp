@@ -1,6 +1,6 @@
 // test_network.cpp -- GPU tests of the operator layer, in the manner of the
 // reference's tests/onnx/test_onnx_inference.cpp, checked against the oracle
-// (oracle/lcml_oracle.c, linked as the checker):
+// (oracle/lcml_oracle.c, linked in as the reference arithmetic):
 //   1. the reference's own fp32 MLP fixture (simple_mlp.onnx.json + weight
 //      blob + input_ref/output_ref, tolerance 1e-3 as the reference uses);
 //   2. the 3-layer FP8 MLP (784->256->128->10, batch 64, per-tensor E4M3
