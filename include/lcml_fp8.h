@@ -73,6 +73,8 @@ extern "C" {
 #define LCML_KERNEL_VALU 3       /* small-M: 128-bit weight streaming, VALU fma, no MFMA */
 #define LCML_KERNEL_MFMA_FP8 4   /* as MFMA with v_mfma_f32_32x32x64_f8f6f4 */
 #define LCML_KERNEL_SKINNY_FP8 5 /* as SKINNY with v_mfma_f32_16x16x128_f8f6f4 */
+#define LCML_KERNEL_MFMA_128 6   /* as MFMA with 128x128 tiles (mid-size GEMMs) */
+#define LCML_KERNEL_MFMA_128_FP8 7 /* as MFMA_128 with v_mfma_f32_32x32x64_f8f6f4 */
 
 /* Message of the last failed call on this thread ("" if none). */
 LCML_API const char *lcml_fp8_last_error(void);
@@ -152,9 +154,9 @@ LCML_API int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N,
  *    broadcast.
  * y: y_dtype LCML_DTYPE_FLOAT or LCML_DTYPE_BFLOAT16 (round to nearest
  *    even), row pitch ldy elements.
- * kernel: LCML_KERNEL_* (AUTO picks SKINNY for M <= 16; for larger M it
- *    picks SKINNY while the 256x256 MFMA grid has fewer than 256 tiles and
- *    a measured cost model of the two kernels favours it, else MFMA).
+ * kernel: LCML_KERNEL_* (AUTO picks SKINNY for M <= 16 and MFMA when the
+ *    256x256 grid has at least 256 tiles; in between, the cheapest of
+ *    SKINNY, MFMA_128 and MFMA by a measured cost model).
  * Replaces the per-thread fma loop nest of Gemm::apply (gemm.cpp:27-325) and
  * MatMul (src/onnx/operators/mat_mul.cpp:51-186) for the DQ->Gemm pattern.
  */

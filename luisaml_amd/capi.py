@@ -21,6 +21,7 @@ DTYPE_FLOAT, DTYPE_BFLOAT16, DTYPE_FLOAT8E4M3FN, DTYPE_FLOAT8E5M2 = 1, 16, 17, 1
 BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_MFMA, KERNEL_SKINNY, KERNEL_VALU, KERNEL_MFMA_FP8, KERNEL_SKINNY_FP8 = 0, 1, 2, 3, 4, 5
+KERNEL_MFMA_128, KERNEL_MFMA_128_FP8 = 6, 7
 DYNAMIC_WORKSPACE_BYTES = 4096
 DYNAMIC_SMALL_MAX = 65536
 PACK_K, PANEL_COLS = 128, 64

@@ -148,20 +148,26 @@ int lcml_fp8_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int w_is
 }
 
 namespace {
-// AUTO's choice between the 256x256-tile MFMA kernel and the skinny kernel.
-// Both times grow about linearly in K.  While the MFMA grid leaves CUs idle
-// (fewer than 256 tiles) it runs one round of tiles, and a 256x256 tile
-// takes 4.3-5.2x as long as a skinny workgroup with 4 row blocks (measured
-// on K = 4096 and 11008); the skinny kernel's time in those units comes
-// from lcml::skinny_row_blocks.  At M = 384: 4096x11008 skinny 71 us
-// against 93 us, 11008x4096 70 us against 205 us.
+// AUTO's kernel for an M x N x K GEMM.  All times grow about linearly in K;
+// in units of one skinny workgroup with 4 row blocks (19 us at K = 4096,
+// 38 us at K = 11008), measured on 4096x11008, 11008x4096 and 4096x4096:
+//   * 256x256 tiles: one round of up to 256 tiles takes 4.5 units;
+//   * 128x128 tiles: 2.2 units per 256 tiles (two workgroups share a CU);
+//   * the skinny kernel: lcml::skinny_row_blocks.
+// M <= 16 always takes the skinny kernel; a 256x256 grid of at least 256
+// tiles keeps the 256x256 kernel.  Examples: 4096x11008 at M = 512: 128x128
+// tiles 64 us against 83 (skinny) and 93 (256x256); 4096x4096 at M = 1024:
+// 46 us against 66 and 91; 11008x4096 at M = 512: skinny 73 us against 91.
 int auto_gemm_kernel(int64_t M, int64_t N, int64_t K) {
     if (M <= 16) return LCML_KERNEL_SKINNY;
     const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
     if (tiles >= 256) return LCML_KERNEL_MFMA;
     double skinny = 0;
     lcml::skinny_row_blocks(M, N, K, &skinny);
-    return skinny < 4.5 ? LCML_KERNEL_SKINNY : LCML_KERNEL_MFMA;
+    const double t128 = (double)((M + 127) / 128 * ((N + 127) / 128));
+    const double small = 2.2 * (t128 > 256 ? t128 / 256 : 1.0);
+    if (skinny <= small && skinny < 4.5) return LCML_KERNEL_SKINNY;
+    return small < 4.5 ? LCML_KERNEL_MFMA_128 : LCML_KERNEL_MFMA;
 }
 }  // namespace
 
@@ -188,10 +194,14 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     switch (kernel) {
     case LCML_KERNEL_MFMA:
     case LCML_KERNEL_MFMA_FP8:
+    case LCML_KERNEL_MFMA_128:
+    case LCML_KERNEL_MFMA_128_FP8:
         // buffer offsets are 32-bit with 0x80000000 as the out-of-range marker
         if ((M - 1) * lda + K >= (int64_t)0x80000000 || lcml_fp8_packed_weight_bytes(K, N) >= (int64_t)0x80000000)
             return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the MFMA kernel", fn);
-        err = lcml::launch_gemm_mfma(M, N, K, a, lda, b_packed, e, kernel == LCML_KERNEL_MFMA, s);
+        err = lcml::launch_gemm_mfma(M, N, K, a, lda, b_packed, e,
+                                     kernel == LCML_KERNEL_MFMA || kernel == LCML_KERNEL_MFMA_128, s,
+                                     kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8);
         break;
     case LCML_KERNEL_SKINNY:
     case LCML_KERNEL_SKINNY_FP8:

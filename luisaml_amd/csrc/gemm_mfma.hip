@@ -473,33 +473,46 @@ constexpr int WM = LCML_GEMM_WM, WN = LCML_GEMM_WN;  // 32x32 blocks per wavefro
 static_assert(WM % 2 == 0, "the NCHW epilogue walks 64-row halves");
 using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
 
-template <bool EXACT, bool CONV>
-hipError_t launch(GemmArgs &g, hipStream_t s) {
-    auto *fn = k_gemm_mfma<WAVES_M, WAVES_N, WM, WN, EXACT, CONV>;
+// 128x128 tiles (2x2 wavefronts of 64x64): a quarter of the work per tile,
+// about half a 256x256 tile's time, and two workgroups per CU (64 KB of
+// LDS each).  It serves mid-size GEMMs whose 256x256 grid would leave most
+// CUs idle.
+using Small = Tile<2, 2, 2, 2>;
+
+template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV>
+hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
+    auto *fn = k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV>;
     static std::atomic<uint64_t> lds_set{0};
-    if (hipError_t err = ensure_dynamic_lds(reinterpret_cast<const void *>(fn), Shipped::LDS_BYTES, lds_set);
+    if (hipError_t err = ensure_dynamic_lds(reinterpret_cast<const void *>(fn), Cfg::LDS_BYTES, lds_set);
         err != hipSuccess)
         return err;
     int64_t Kp = pad_to(g.K, kPackK), Np = pad_to(g.N, kPanelCols);
     g.KC = Kp / 16;
     g.npanels = Np / 64;
-    g.tiles_m = (int)((g.M + Shipped::BM - 1) / Shipped::BM);
-    g.tiles_n = (int)((g.N + Shipped::BN - 1) / Shipped::BN);
+    g.tiles_m = (int)((g.M + Cfg::BM - 1) / Cfg::BM);
+    g.tiles_n = (int)((g.N + Cfg::BN - 1) / Cfg::BN);
     g.nk = (int)(Kp / BK);
     g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
-    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Shipped::NT),
-                       Shipped::LDS_BYTES, s, g);
+    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT),
+                       Cfg::LDS_BYTES, s, g);
     return hipGetLastError();
+}
+
+template <bool EXACT, bool CONV>
+hipError_t launch(GemmArgs &g, hipStream_t s) {
+    return launch_cfg<Shipped, WAVES_M, WAVES_N, WM, WN, EXACT, CONV>(g, s);
 }
 
 }  // namespace
 
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
-                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
+                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s, bool small_tiles) {
     GemmArgs g = {};
     g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
     g.a_bytes = (uint32_t)((M - 1) * lda + K);
     g.e = e;
+    if (small_tiles)
+        return exact ? launch_cfg<Small, 2, 2, 2, 2, true, false>(g, s) : launch_cfg<Small, 2, 2, 2, 2, false, false>(g, s);
     return exact ? launch<true, false>(g, s) : launch<false, false>(g, s);
 }
 

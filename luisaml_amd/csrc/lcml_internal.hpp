@@ -31,8 +31,10 @@ hipError_t launch_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int
                                 uint8_t *w, hipStream_t s);
 
 // exact: bf16 MFMAs on widened E4M3 (fp32-accurate); else native FP8 MFMAs
+// small_tiles: 128x128 workgroup tiles instead of 256x256
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
-                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s);
+                            const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s,
+                            bool small_tiles = false);
 // implicit-im2col FP8 convolution on the MFMA tile kernel: x_nhwc E4M3
 // [Nb][H][W][C] ((C/group) % 16 == 0), bp = conv weights packed per group
 // with K = (kh, kw, c), output NCHW [Nb][Cout][OH][OW] through the epilogue

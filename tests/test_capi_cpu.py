@@ -35,6 +35,8 @@ def test_abi_version():
 
 def test_python_constants_match_header():
     assert capi.DYNAMIC_WORKSPACE_BYTES == header_define("LCML_FP8_DYNAMIC_WORKSPACE_BYTES")
+    for name in ("AUTO", "MFMA", "SKINNY", "VALU", "MFMA_FP8", "SKINNY_FP8", "MFMA_128", "MFMA_128_FP8"):
+        assert getattr(capi, "KERNEL_" + name) == header_define("LCML_KERNEL_" + name), name
 
 
 def test_packed_weight_bytes():

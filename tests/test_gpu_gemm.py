@@ -12,7 +12,8 @@ from tests.gemm_cases import assert_close, make_case, reference
 pytestmark = pytest.mark.gpu
 
 KERNELS = {"mfma": capi.KERNEL_MFMA, "skinny": capi.KERNEL_SKINNY, "valu": capi.KERNEL_VALU,
-           "mfma_fp8": capi.KERNEL_MFMA_FP8, "skinny_fp8": capi.KERNEL_SKINNY_FP8}
+           "mfma_fp8": capi.KERNEL_MFMA_FP8, "skinny_fp8": capi.KERNEL_SKINNY_FP8,
+           "mfma_128": capi.KERNEL_MFMA_128, "mfma_128_fp8": capi.KERNEL_MFMA_128_FP8}
 
 
 def run(c, kernel, bias=None, alpha=1.0, beta=1.0, act=capi.ACT_NONE, out_dtype=torch.float32, dev=None):
@@ -25,9 +26,10 @@ def run(c, kernel, bias=None, alpha=1.0, beta=1.0, act=capi.ACT_NONE, out_dtype=
 @pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 768, 1024), (300, 500, 784), (1, 64, 128),
                                    (257, 100, 2304), (64, 10, 128), (1024, 1024, 4096)])
 @pytest.mark.parametrize("per_channel", [True, False])
-def test_mfma_shapes(dev, M, N, K, per_channel):
+@pytest.mark.parametrize("kernel", ["mfma", "mfma_128"])
+def test_mfma_shapes(dev, M, N, K, per_channel, kernel):
     c = make_case(M, N, K, seed=M + N + K, per_channel=per_channel, dev=dev)
-    y = run(c, capi.KERNEL_MFMA, dev=dev).cpu().numpy()
+    y = run(c, KERNELS[kernel], dev=dev).cpu().numpy()
     ref, bound = reference(c)
     assert_close(y, ref, bound)
 
@@ -79,7 +81,7 @@ def test_medium_m_epilogue(dev, M):
 @pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
 @pytest.mark.parametrize("w_is_nk", [False, True])
 def test_weight_layouts(dev, kernel, w_is_nk):
-    M = 16 if kernel != "mfma" else 200
+    M = 16 if not kernel.startswith("mfma") else 200
     c = make_case(M, 320, 512, seed=5, w_is_nk=w_is_nk, dev=dev)
     y = run(c, KERNELS[kernel], dev=dev).cpu().numpy()
     ref, bound = reference(c)
@@ -95,10 +97,10 @@ def make_bias(kind, M, N, seed=1):
     return (rng.standard_normal(shape) * 0.01).astype(np.float32)
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_128"])
 @pytest.mark.parametrize("bias_kind", BIAS_SHAPES)
 def test_epilogue_bias_broadcast(dev, kernel, bias_kind):
-    M = 12 if kernel != "mfma" else 130
+    M = 12 if not kernel.startswith("mfma") else 130
     N = 192
     c = make_case(M, N, 256, seed=7, dev=dev)
     bias = make_bias(bias_kind, M, N)
@@ -107,10 +109,10 @@ def test_epilogue_bias_broadcast(dev, kernel, bias_kind):
     assert_close(y, ref, bound)
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_128"])
 @pytest.mark.parametrize("act", [capi.ACT_RELU, capi.ACT_GELU_ERF, capi.ACT_GELU_TANH])
 def test_epilogue_activation(dev, kernel, act):
-    M = 16 if kernel != "mfma" else 256
+    M = 16 if not kernel.startswith("mfma") else 256
     c = make_case(M, 256, 512, seed=9, dev=dev)
     bias = make_bias("N", M, 256, seed=3)
     y = run(c, KERNELS[kernel], bias=bias, act=act, dev=dev).cpu().numpy()
@@ -118,11 +120,11 @@ def test_epilogue_activation(dev, kernel, act):
     assert_close(y, ref, bound, act=act)
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu"])
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_128"])
 @pytest.mark.parametrize("act", [capi.ACT_NONE, capi.ACT_GELU_ERF])
 def test_bf16_output_is_rne_of_fp32(dev, kernel, act):
     """bf16 output is bit-exactly bf16_rne of the same kernel's fp32 output."""
-    M = 16 if kernel != "mfma" else 384
+    M = 16 if not kernel.startswith("mfma") else 384
     c = make_case(M, 448, 1024, seed=13, dev=dev)
     bias = make_bias("N", M, 448, seed=4)
     y32 = run(c, KERNELS[kernel], bias=bias, act=act, dev=dev).cpu().numpy()
@@ -165,7 +167,7 @@ def test_nan_propagates(dev):
     qb[40, 77] = 0xFF  # [K, N]: column 77
     c.d_qa = torch.from_numpy(qa).to(dev)
     c.d_bp = capi.pack_weight(torch.from_numpy(qb).to(dev), False)
-    for k in ("mfma", "skinny", "valu"):
+    for k in ("mfma", "skinny", "valu", "mfma_128"):
         y = run(c, KERNELS[k], dev=dev).cpu().numpy()
         assert np.isnan(y[3]).all(), k
         assert np.isnan(y[:, 77]).all(), k
@@ -182,7 +184,7 @@ def test_errors_are_reported(dev):
     assert e.value.code == capi.ERR_UNSUPPORTED
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_fp8", "skinny_fp8"])
+@pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_fp8", "skinny_fp8", "mfma_128", "mfma_128_fp8"])
 def test_identity_reproduces_every_code(dev, kernel):
     """One-hot A rows (1.0 = 0x38) pick single weights: y[m, n] = to_float(B[m, n])
     exactly, for all 254 non-NaN E4M3 codes, through each kernel's operand
@@ -207,7 +209,7 @@ def test_identity_reproduces_every_code(dev, kernel):
     assert np.array_equal(y[nz].view(np.uint32), ref[nz].view(np.uint32))
 
 
-@pytest.mark.parametrize("kernel", ["mfma_fp8", "skinny_fp8"])
+@pytest.mark.parametrize("kernel", ["mfma_fp8", "skinny_fp8", "mfma_128_fp8"])
 def test_native_fp8_mfma_precision_is_documented(dev, kernel):
     """The opt-in native-FP8-MFMA kernels stay inside the elementwise bound and
     within 3e-5 relative Frobenius (gfx950 FP8 MFMA block truncation)."""
