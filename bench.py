@@ -265,15 +265,17 @@ def main() -> int:
         lib_ref["small_m_fp8_scaled_mm_gbs"] = {m: round(gemm_kernel_bytes(int(m)) / (t * 1e-6) / 1e9, 1)
                                                 for m, t in fp8_us.items()}
         # medium M on the same linear: AUTO (the skinny kernel with 2 or 4
-        # row blocks per workgroup here) against the 256x256-tile kernel and
-        # the library, E4M3 activations in, bf16 out
+        # row blocks per workgroup, or 128x128 tiles) against the 256x256-
+        # and 128x128-tile kernels and the library, E4M3 activations in, bf16
+        # out
         med = {}
         for M in MEDIUM_MS:
             qx = capi.quantize(torch.from_numpy(synth.normal(400 + M, (M, K))).to(dev), one)
             x8 = qx.view(torch.float8_e4m3fn)
             yv = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             row = {}
-            for name, kern in (("auto_us", capi.KERNEL_AUTO), ("tile_kernel_us", capi.KERNEL_MFMA)):
+            for name, kern in (("auto_us", capi.KERNEL_AUTO), ("tile_kernel_us", capi.KERNEL_MFMA),
+                               ("tile128_kernel_us", capi.KERNEL_MFMA_128)):
                 gm = capture(lambda i, kern=kern: capi.gemm(qx, one, packed[i % N_WEIGHT_COPIES], d_sw, N, K,
                                                              out=yv, kernel=kern), 3 * args.steps)
                 gm.replay()
