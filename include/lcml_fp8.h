@@ -238,7 +238,9 @@ LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t c
  * channels g*cout/group .., conv.cpp:139,158).
  * w_packed: lcml_fp8_pack_conv_weight output.  bias: cout floats or NULL.
  * y: NCHW [n][cout][oh][ow], y_dtype LCML_DTYPE_FLOAT or BFLOAT16.
- * kernel: LCML_KERNEL_AUTO / MFMA (exact bf16 matrix cores) or MFMA_FP8.
+ * kernel: LCML_KERNEL_AUTO / MFMA / MFMA_128 (exact bf16 matrix cores,
+ *    256x256 or 128x128 tiles) or MFMA_FP8 / MFMA_128_FP8; AUTO takes the
+ *    128x128 tiles when the 256x256 grid (times the groups) is small.
  * Replaces Conv::apply (src/onnx/operators/conv.cpp:115-207) for the
  * DQ(x), DQ(W) -> Conv [-> Relu/Gelu] pattern.
  */

@@ -343,9 +343,17 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
     if (n * h * w * c >= (int64_t)1 << 31 || M >= (int64_t)1 << 31 ||
         lcml_fp8_packed_conv_weight_bytes(cout, c / group, kh, kw, group) >= (int64_t)1 << 31)
         return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB", fn);
-    if (kernel == LCML_KERNEL_AUTO) kernel = LCML_KERNEL_MFMA;
-    if (kernel != LCML_KERNEL_MFMA && kernel != LCML_KERNEL_MFMA_FP8)
-        return fail(LCML_ERR_UNSUPPORTED, "%s: kernel %d (AUTO, MFMA or MFMA_FP8)", fn, kernel);
+    if (kernel == LCML_KERNEL_AUTO) {
+        // as auto_gemm_kernel without the skinny kernel; groups add grid rows
+        const int64_t N = cout / group;
+        const double big = (double)((M + 255) / 256 * ((N + 255) / 256) * group);
+        const double t128 = (double)((M + 127) / 128 * ((N + 127) / 128) * group);
+        const double small = 2.2 * (t128 > 256 ? t128 / 256 : 1.0);
+        kernel = big < 256 && small < 4.5 ? LCML_KERNEL_MFMA_128 : LCML_KERNEL_MFMA;
+    }
+    if (kernel != LCML_KERNEL_MFMA && kernel != LCML_KERNEL_MFMA_FP8 && kernel != LCML_KERNEL_MFMA_128 &&
+        kernel != LCML_KERNEL_MFMA_128_FP8)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: kernel %d (AUTO or one of the MFMA tile kernels)", fn, kernel);
     lcml::Epilogue e;
     if (int rc = make_epilogue(e, fn, M, cout, x_scale, w_scale, w_scale_per_channel, 1.0f, bias, 1, cout, 0, 1.0f,
                                act, y, y_dtype, cout))
@@ -360,8 +368,10 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
         return fail(LCML_ERR_INVALID_ARG, "%s: x_nhwc and w_packed must be 16-byte aligned", fn);
     return hip_status(lcml::launch_conv_mfma(x_nhwc, n, (int)c, (int)h, (int)w, w_packed, (int)cout, (int)kh, (int)kw,
                                              (int)stride_h, (int)stride_w, (int)pad_h, (int)pad_w, (int)dil_h,
-                                             (int)dil_w, (int)group, (int)oh, (int)ow, e, kernel == LCML_KERNEL_MFMA,
-                                             (hipStream_t)stream),
+                                             (int)dil_w, (int)group, (int)oh, (int)ow, e,
+                                             kernel == LCML_KERNEL_MFMA || kernel == LCML_KERNEL_MFMA_128,
+                                             (hipStream_t)stream,
+                                             kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8),
                       fn);
 }
 

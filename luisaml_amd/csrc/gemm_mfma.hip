@@ -518,7 +518,7 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
 
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
                             int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int group, int OH, int OW,
-                            const Epilogue &e, bool exact, hipStream_t s) {
+                            const Epilogue &e, bool exact, hipStream_t s, bool small_tiles) {
     GemmArgs g = {};
     const int Cg = C / group;
     g.cv = ConvGeom{H, W, Cg, C, Cout, OH, OW, KH, KW, sh, sw, ph, pw, dh, dw};
@@ -526,6 +526,8 @@ hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int
     g.a = x_nhwc; g.lda = 0; g.bp = bp;
     g.a_bytes = (uint32_t)(Nb * H * W * C);
     g.e = e;
+    if (small_tiles)
+        return exact ? launch_cfg<Small, 2, 2, 2, 2, true, true>(g, s) : launch_cfg<Small, 2, 2, 2, 2, false, true>(g, s);
     return exact ? launch<true, true>(g, s) : launch<false, true>(g, s);
 }
 

@@ -42,7 +42,8 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
 // scale and bias pointers cover all Cout channels)
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
                             int KH, int KW, int sh, int sw, int ph, int pw, int dh, int dw, int group, int OH, int OW,
-                            const Epilogue &e, bool exact, hipStream_t s);
+                            const Epilogue &e, bool exact, hipStream_t s,
+                            bool small_tiles = false);
 // NCHW fp32 -> NHWC E4M3 with a per-tensor scale: scale[0], or amax/448 from
 // npart partial maxima when part is given (then written to scale_out if
 // non-null)

@@ -99,13 +99,14 @@ def reference(x, qw, ws, bias, stride, pad, dil, act, per_channel=True, group=1)
 
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("act", [capi.ACT_NONE, capi.ACT_RELU])
-def test_conv_matches_oracle(dev, case, act):
+@pytest.mark.parametrize("kernel", [capi.KERNEL_AUTO, capi.KERNEL_MFMA, capi.KERNEL_MFMA_128])
+def test_conv_matches_oracle(dev, case, act, kernel):
     n, c, h, w, cout, kh, kw, stride, pad, dil = case
     x, qw, ws = conv_case(n, c, h, w, cout, kh, kw, seed=n * 7 + c + cout, dev=dev)
     bias = synth.normal(77, (cout,), std=0.01)
     xq, sx = capi.quantize_nhwc(to_dev(x, dev))
     y = capi.conv2d(xq, sx, capi.pack_conv_weight(to_dev(qw, dev)), to_dev(ws, dev), cout, (kh, kw),
-                    (stride, stride), (pad, pad), (dil, dil), bias=to_dev(bias, dev), act=act)
+                    (stride, stride), (pad, pad), (dil, dil), bias=to_dev(bias, dev), act=act, kernel=kernel)
     ref, bound = reference(x, qw, ws, bias, stride, pad, dil, act)
     assert y.shape == ref.shape
     assert_close(y.cpu().numpy(), ref, bound, act=act)
@@ -113,7 +114,8 @@ def test_conv_matches_oracle(dev, case, act):
 
 @pytest.mark.parametrize("case", [(2, 32, 9, 11, 24, 3, 3, 1, 1, 1, 2), (1, 64, 10, 10, 64, 3, 3, 2, 1, 1, 4),
                                   (1, 48, 8, 8, 30, 1, 1, 1, 0, 1, 3), (2, 128, 7, 7, 256, 3, 3, 1, 2, 2, 8)])
-@pytest.mark.parametrize("kernel", [capi.KERNEL_MFMA, capi.KERNEL_MFMA_FP8])
+@pytest.mark.parametrize("kernel", [capi.KERNEL_MFMA, capi.KERNEL_MFMA_FP8, capi.KERNEL_MFMA_128,
+                                    capi.KERNEL_MFMA_128_FP8])
 def test_grouped_conv_matches_oracle(dev, case, kernel):
     """Grouped FP8 conv: each group's GEMM reads its channel slice and writes
     its output-channel slice (conv.cpp:139,158)."""
@@ -125,7 +127,7 @@ def test_grouped_conv_matches_oracle(dev, case, kernel):
                     (stride, stride), (pad, pad), (dil, dil), bias=to_dev(bias, dev), act=capi.ACT_RELU,
                     kernel=kernel, group=group)
     ref, bound = reference(x, qw, ws, bias, stride, pad, dil, capi.ACT_RELU, group=group)
-    if kernel == capi.KERNEL_MFMA:
+    if kernel in (capi.KERNEL_MFMA, capi.KERNEL_MFMA_128):
         assert_close(y.cpu().numpy(), ref, bound, act=capi.ACT_RELU)
     else:
         rel = np.linalg.norm(y.cpu().numpy() - ref) / np.linalg.norm(ref)
