@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle
-from luisaml_amd import capi
+from luisaml_amd import capi, synth
 from tests.gemm_cases import assert_close, make_case, reference
 
 pytestmark = pytest.mark.gpu
@@ -220,3 +220,29 @@ def test_native_fp8_mfma_precision_is_documented(dev, kernel):
     assert np.all(np.abs(y - ref) <= 1e-4 * bound)
     rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     assert rel < 3e-5
+
+
+def test_concurrent_streams_match_serial(dev):
+    """The entry points keep no shared mutable state between calls: the same
+    GEMMs (tile, 128-tile, skinny, fused dynamic) issued on two streams at
+    once give the bits they give one after another on one stream."""
+    cases = [make_case(M, N, K, seed=50 + M, dev=dev) for M, N, K in ((300, 500, 784), (24, 1100, 512),
+                                                                      (1024, 640, 256), (4, 2048, 1024))]
+    kernels = [capi.KERNEL_MFMA, capi.KERNEL_SKINNY, capi.KERNEL_MFMA_128, capi.KERNEL_SKINNY]
+    x4 = torch.from_numpy(synth.normal(59, (4, 1024))).to(dev)
+    serial = [run(c, k, dev=dev) for c, k in zip(cases, kernels)]
+    serial.append(capi.gemm_dynamic(x4, cases[3].d_bp, cases[3].d_sb, cases[3].N, cases[3].K))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = [None] * 5
+    for rep in range(3):
+        for i, (c, k) in enumerate(zip(cases, kernels)):
+            with torch.cuda.stream(streams[i % 2]):
+                outs[i] = capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, kernel=k)
+        with torch.cuda.stream(streams[1]):
+            outs[4] = capi.gemm_dynamic(x4, cases[3].d_bp, cases[3].d_sb, cases[3].N, cases[3].K)
+        torch.cuda.synchronize()
+        for i in range(5):
+            assert torch.equal(outs[i].view(torch.int32), serial[i].view(torch.int32)), (rep, i)
