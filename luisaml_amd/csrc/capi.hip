@@ -199,6 +199,8 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
         // buffer offsets are 32-bit with 0x80000000 as the out-of-range marker
         if ((M - 1) * lda + K >= (int64_t)0x80000000 || lcml_fp8_packed_weight_bytes(K, N) >= (int64_t)0x80000000)
             return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the MFMA kernel", fn);
+        if ((M + 127) / 128 * ((N + 127) / 128) >= (int64_t)0x80000000)
+            return fail(LCML_ERR_UNSUPPORTED, "%s: M=%lld N=%lld exceeds the tile grid", fn, (long long)M, (long long)N);
         err = lcml::launch_gemm_mfma(M, N, K, a, lda, b_packed, e,
                                      kernel == LCML_KERNEL_MFMA || kernel == LCML_KERNEL_MFMA_128, s,
                                      kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8);
