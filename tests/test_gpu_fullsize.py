@@ -114,3 +114,33 @@ def test_conv3x3_resnet_one_image(dev):
     ref = oracle.conv2d(A, B, bias, pads=(1, 1), act=oracle.ACT_RELU)
     bound = oracle.conv2d(np.abs(A), np.abs(B), np.abs(bias), pads=(1, 1))
     assert_close(y[img:img + 1].cpu().numpy(), ref, bound, act=oracle.ACT_RELU)
+
+
+@pytest.mark.parametrize("M", [64, 256, 512])
+def test_decode_linear_medium_m_auto(dev, decode_weight, M):
+    """The same 4096x11008 linear past decode sizes, through AUTO (skinny
+    kernel with row groups at M=64, 128x128 tiles at M=256 and 512), fp32
+    out; 12 sampled rows against the oracle."""
+    qw, sw, bp, d_sw = decode_weight
+    x = synth.normal(700 + M, (M, 4096))
+    y = capi.gemm_dynamic(to_dev(x, dev), bp, d_sw, 11008, 4096, out_dtype=torch.float32)
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    rows = np.unique(np.array([0, 1, 15, 16, 31, 32, 63, M // 2, M - 17, M - 2, M - 1]) % M)
+    ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw)
+    assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B))
+
+
+def test_mid_size_gemm_128_tiles_sampled_rows(dev):
+    """M=2048 x 4096 -> 4096, where AUTO takes the 128x128 tiles; the 256x256
+    kernel's output on the same operands agrees within the bound too."""
+    x = synth.normal(710, (2048, 4096))
+    w = synth.normal(711, (4096, 4096), std=0.02)
+    qw, sw, bp, d_sw = per_channel_weight(w, dev)
+    qa, sa = capi.quantize_dynamic(to_dev(x, dev))
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    rows = np.array([0, 127, 128, 1000, 2047])
+    ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw)
+    bound = oracle.gemm_abs_bound(A, B)
+    for kernel in (capi.KERNEL_AUTO, capi.KERNEL_MFMA_128, capi.KERNEL_MFMA):
+        y = capi.gemm(qa, sa, bp, d_sw, 4096, 4096, out_dtype=torch.float32, kernel=kernel)
+        assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, bound)
