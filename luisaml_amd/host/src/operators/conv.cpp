@@ -39,27 +39,57 @@ ConvAttrs conv_attrs(const Node &node, const char *op) {
     return a;
 }
 
-// Conv(X fp32 [n,c,h,w], W fp32 [cout, c/group, kh, kw] [, B]) -> Y fp32
+// Conv(X [n,c,h,w], W [cout, c/group, kh, kw] [, B]) -> Y, all of one element
+// type: float, or an fp8 type (FLOAT8E4M3FN / FLOAT8E5M2) as the reference
+// also accepts (conv.cpp:65-70, 84-105: fp8 operands decoded, the result
+// encoded back).  The fp8 form decodes X, W and B exactly to fp32, runs the
+// fp32 convolution and encodes Y with the reference's CPU encoder; the
+// reference accumulates fp8 convolutions in half precision and encodes with
+// its half-precision device codec, so results can differ from it by the
+// rounding of those half steps (the fp32 sum is the more accurate one).
 class Conv : public StreamOperator {
     ConvAttrs a_;
+    std::unique_ptr<DeviceBuffer> f32_;  // fp8 form: fp32 copies of X, W, B and Y
+    size_t f32_bytes_ = 0;
 
 public:
     explicit Conv(ConvAttrs a) : StreamOperator("Conv"), a_(a) {}
     void forward(std::span<std::reference_wrapper<ITensor>> inputs,
                  std::span<std::reference_wrapper<ITensor>> outputs) override {
         ITensor &X = inputs[0], &Wt = inputs[1], &Y = outputs[0];
-        LCML_ASSERT(is_type<float>(X) && is_type<float>(Wt) && is_type<float>(Y),
-                    "Conv: float tensors expected (FP8 convolutions run through the fused FP8 path)");
+        ITensor *B = inputs.size() > 2 ? &inputs[2].get() : nullptr;
+        const int dt = fp8_path_dtype(X);
+        LCML_ASSERT(dt != 0 && fp8_path_dtype(Wt) == dt && fp8_path_dtype(Y) == dt && (!B || fp8_path_dtype(*B) == dt),
+                    "Conv: X, W, B and Y must all be float, FLOAT8E4M3FN or FLOAT8E5M2");
         LCML_ASSERT(X.ndim() == 4 && Wt.ndim() == 4 && Y.ndim() == 4, "Conv: only 2-D (NCHW) convolution");
-        const float *bias = inputs.size() > 2 ? static_cast<const float *>(inputs[2].get().device_data()) : nullptr;
         const int64_t kh = a_.kh ? a_.kh : Wt.shape(2), kw = a_.kw ? a_.kw : Wt.shape(3);
         LCML_ASSERT(Wt.shape(2) == kh && Wt.shape(3) == kw, "Conv: kernel_shape does not match W");
-        check(lcml_fp8_conv2d_f32(static_cast<const float *>(X.device_data()),
-                                  static_cast<const float *>(Wt.device_data()), bias,
-                                  static_cast<float *>(Y.device_data()), X.shape(0), X.shape(1), X.shape(2),
-                                  X.shape(3), Wt.shape(0), kh, kw, a_.sh, a_.sw, a_.ph, a_.pw, a_.dh, a_.dw, a_.group,
-                                  Y.shape(2), Y.shape(3), LCML_ACT_NONE, stream_),
+        const float *x = static_cast<const float *>(X.device_data());
+        const float *w = static_cast<const float *>(Wt.device_data());
+        const float *bias = B ? static_cast<const float *>(B->device_data()) : nullptr;
+        float *y = static_cast<float *>(Y.device_data());
+        if (dt != LCML_DTYPE_FLOAT) {
+            const size_t nx = X.size(), nw = Wt.size(), nb = B ? B->size() : 0, ny = Y.size();
+            const size_t need = (nx + nw + nb + ny) * sizeof(float);
+            if (!f32_ || f32_bytes_ < need) {
+                f32_ = std::make_unique<DeviceBuffer>(need);
+                f32_bytes_ = need;
+            }
+            float *fx = static_cast<float *>(f32_->data()), *fw = fx + nx, *fb = fw + nw, *fy = fb + nb;
+            check(lcml_fp8_cast(X.device_data(), dt, fx, LCML_DTYPE_FLOAT, (int64_t)nx, stream_), "Conv");
+            check(lcml_fp8_cast(Wt.device_data(), dt, fw, LCML_DTYPE_FLOAT, (int64_t)nw, stream_), "Conv");
+            if (B) check(lcml_fp8_cast(B->device_data(), dt, fb, LCML_DTYPE_FLOAT, (int64_t)nb, stream_), "Conv");
+            x = fx;
+            w = fw;
+            bias = B ? fb : nullptr;
+            y = fy;
+        }
+        check(lcml_fp8_conv2d_f32(x, w, bias, y, X.shape(0), X.shape(1), X.shape(2), X.shape(3), Wt.shape(0), kh, kw,
+                                  a_.sh, a_.sw, a_.ph, a_.pw, a_.dh, a_.dw, a_.group, Y.shape(2), Y.shape(3),
+                                  LCML_ACT_NONE, stream_),
               "Conv");
+        if (dt != LCML_DTYPE_FLOAT)
+            check(lcml_fp8_cast(y, LCML_DTYPE_FLOAT, Y.device_data(), dt, (int64_t)Y.size(), stream_), "Conv");
     }
 };
 

@@ -882,6 +882,73 @@ static void test_batched_matmul() {
     }
 }
 
+// Conv on fp8 tensors (the reference accepts FLOAT8E4M3FN / FLOAT8E5M2 X, W,
+// B, Y: conv.cpp:65-105): Cast(x) -> Conv(x8, W8, B8) -> y8 -> Cast(float),
+// against the oracle's fp32 conv of the decoded operands, encoded with the
+// same CPU encoder.  Codes agree except, rarely, one step apart where the
+// fp32 value sits next to a rounding midpoint and the summation orders
+// differ in the last bit.
+static void test_fp8_tensor_conv(bool e5m2) {
+    std::printf("[13] Conv on %s tensors (decode, fp32 conv, encode)\n", e5m2 ? "FLOAT8E5M2" : "FLOAT8E4M3FN");
+    const int64_t Nb = 2, C = 8, H = 9, W = 7, CO = 6, KH = 3, KW = 3, G = 2;
+    const int64_t OH = H, OW = W;  // stride 1, pad 1
+    const DataType dt = e5m2 ? DataType::FLOAT8E5M2 : DataType::FLOAT8E4M3FN;
+    auto enc = [&](float v) { return e5m2 ? orc_e5m2_from_float(v) : orc_e4m3_from_float(v); };
+    auto dec = [&](uint8_t c) { return e5m2 ? orc_e5m2_to_float(c) : orc_e4m3_to_float(c); };
+    auto x = normals(140 + e5m2, (size_t)(Nb * C * H * W), 2.0f);
+    auto wf = normals(142 + e5m2, (size_t)(CO * (C / G) * KH * KW), 0.5f);
+    auto bf = normals(144 + e5m2, (size_t)CO, 0.5f);
+    std::vector<uint8_t> w8(wf.size()), b8(bf.size());
+    for (size_t i = 0; i < wf.size(); ++i) w8[i] = enc(wf[i]);
+    for (size_t i = 0; i < bf.size(); ++i) b8[i] = enc(bf[i]);
+    Graph g("conv8");
+    Blob blob;
+    var(g, "x", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    var(g, "x8", dt, {(size_t)Nb, (size_t)C, (size_t)H, (size_t)W});
+    blob_var(g, blob, "W8", dt, {(size_t)CO, (size_t)(C / G), (size_t)KH, (size_t)KW}, w8.data(), w8.size());
+    blob_var(g, blob, "B8", dt, {(size_t)CO}, b8.data(), b8.size());
+    var(g, "y8", dt, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
+    var(g, "y", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OH, (size_t)OW});
+    node(g, "Cast", {"x"}, {"x8"}, {Attribute{"to", (int32_t)(e5m2 ? 19 : 17)}});
+    node(g, "Conv", {"x8", "W8", "B8"}, {"y8"},
+         {Attribute{"group", (int32_t)G}, Attribute{"pads", std::vector<int32_t>{1, 1, 1, 1}}});
+    node(g, "Cast", {"y8"}, {"y"}, {Attribute{"to", (int32_t)1}});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    DeviceBuffer wb(blob.bytes.size());
+    CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+    auto xt = upload(x, {(uint32_t)Nb, (uint32_t)C, (uint32_t)H, (uint32_t)W});
+    auto yt = make_device_tensor<float>({(uint32_t)Nb, (uint32_t)CO, (uint32_t)OH, (uint32_t)OW});
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_weight_buffer(wb.data(), blob.bytes.size());
+    net.set_input("x", *xt);
+    net.set_output("y", *yt);
+    net.forward();
+    auto y = download<float>(*yt);
+    std::vector<float> xd(x.size()), wd(wf.size()), bd(bf.size()), ref(y.size());
+    for (size_t i = 0; i < x.size(); ++i) xd[i] = dec(enc(x[i]));
+    for (size_t i = 0; i < wf.size(); ++i) wd[i] = dec(w8[i]);
+    for (size_t i = 0; i < bf.size(); ++i) bd[i] = dec(b8[i]);
+    orc_conv2d(xd.data(), wd.data(), bd.data(), ref.data(), Nb, C, H, W, CO, KH, KW, 1, 1, 1, 1, 1, 1, G, OH, OW,
+               LCML_ACT_NONE);
+    size_t exact = 0, near = 0, far = 0;
+    for (size_t i = 0; i < y.size(); ++i) {
+        const uint8_t want = enc(ref[i]), got = enc(y[i]);  // y holds decoded codes: re-encoding is exact
+        if (want == got) {
+            ++exact;
+        } else if ((want & 0x80) == (got & 0x80) && std::abs((int)(want & 0x7f) - (int)(got & 0x7f)) == 1) {
+            ++near;
+        } else {
+            ++far;
+        }
+    }
+    std::printf("    %zu codes equal, %zu one step apart, %zu further\n", exact, near, far);
+    CHECK(far == 0 && near * 200 <= y.size());
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -903,6 +970,8 @@ int main(int argc, char **argv) {
         test_qdq_conv(true, 2);
         test_f32_grouped_conv();
         test_batched_matmul();
+        test_fp8_tensor_conv(false);
+        test_fp8_tensor_conv(true);
         test_e5m2_qdq_cast();
         test_elementwise();
         test_memory_planner();
