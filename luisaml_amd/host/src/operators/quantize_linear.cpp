@@ -125,10 +125,16 @@ public:
 
 }  // namespace
 
+// opset 21's blocked quantisation (block_size > 0) is outside this path:
+// per-tensor and per-axis scales only
 REGISTER_TO_DEFAULT_OPSET(QuantizeLinear) {
+    LCML_ASSERT(attr_int(node, "block_size", 0) == 0, "QuantizeLinear: blocked quantisation is not supported");
     return std::make_unique<QuantizeLinear>(attr_int(node, "axis", 1), attr_int(node, "saturate", 1));
 };
-REGISTER_TO_DEFAULT_OPSET(DequantizeLinear) { return std::make_unique<DequantizeLinear>(attr_int(node, "axis", 1)); };
+REGISTER_TO_DEFAULT_OPSET(DequantizeLinear) {
+    LCML_ASSERT(attr_int(node, "block_size", 0) == 0, "DequantizeLinear: blocked quantisation is not supported");
+    return std::make_unique<DequantizeLinear>(attr_int(node, "axis", 1));
+};
 REGISTER_TO_DEFAULT_OPSET(DynamicQuantizeLinear) { return std::make_unique<DynamicQuantizeLinear>(); };
 REGISTER_TO_DEFAULT_OPSET(Cast) {
     return std::make_unique<Cast>((DataType)attr_int(node, "to", 1), attr_int(node, "saturate", 1));

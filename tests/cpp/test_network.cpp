@@ -587,6 +587,30 @@ static void test_errors() {
     net.set_input("x", *xt);
     net.set_output("y", *yt);
     CHECK(throws([&] { net.forward(); }));  // Weight buffer size mismatch
+    // blocked quantisation (opset 21 block_size) is rejected, not silently run per-axis
+    for (const char *op : {"QuantizeLinear", "DequantizeLinear"}) {
+        bool q = op[0] == 'Q';
+        Graph gb("b");
+        var(gb, "x", q ? DataType::FLOAT : DataType::FLOAT8E4M3FN, {2, 64});
+        raw_var(gb, "s", DataType::FLOAT, {2, 2}, std::vector<float>(4, 1.0f).data(), 16);
+        var(gb, "y", q ? DataType::FLOAT8E4M3FN : DataType::FLOAT, {2, 64});
+        node(gb, op, {"x", "s"}, {"y"}, {Attribute{"axis", (int32_t)1}, Attribute{"block_size", (int32_t)32}});
+        gb.add_input("x");
+        gb.add_output("y");
+        Model mb(21, "test", "1");
+        mb.set_graph(std::move(gb));
+        auto xb = q ? make_device_tensor<float>({2, 64}) : nullptr;
+        auto xq = q ? nullptr : make_device_tensor<FP8E4M3FN>({2, 64});
+        auto yq = q ? make_device_tensor<FP8E4M3FN>({2, 64}) : nullptr;
+        auto yb = q ? nullptr : make_device_tensor<float>({2, 64});
+        CHECK(throws([&] {
+            NetworkInstance nb;
+            nb.set_model(std::move(mb));
+            if (q) nb.set_input("x", *xb), nb.set_output("y", *yq);
+            else nb.set_input("x", *xq), nb.set_output("y", *yb);
+            nb.forward();
+        }));
+    }
 }
 
 static bool same_f32(float a, float b) { return std::isnan(b) ? std::isnan(a) : std::memcmp(&a, &b, 4) == 0; }
