@@ -493,8 +493,12 @@ hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
     g.tiles_n = (int)((g.N + Cfg::BN - 1) / Cfg::BN);
     g.nk = (int)(Kp / BK);
     g.b_bytes = (uint32_t)(g.npanels * g.KC * 1024);
-    hipLaunchKernelGGL(fn, dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT),
-                       Cfg::LDS_BYTES, s, g);
+    // launched by name, as every other kernel here: a launch through the
+    // pointer variable returned success without running the kernel when the
+    // host pass was built with -fsanitize=address,undefined
+    hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV>),
+                       dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES,
+                       s, g);
     return hipGetLastError();
 }
 
