@@ -2,7 +2,7 @@
 //
 // Y[M,N] = epilogue( A[M,K] (E4M3, row-major) x B[K,N] (E4M3, packed panels) )
 //
-// Workgroup tile 256x256, K step 128, 512 threads = 8 wavefronts laid out
+// Workgroup tile 256x256, K step 64, 512 threads = 8 wavefronts laid out
 // 2 (M) x 4 (N); each wavefront owns a 128x64 sub-tile = 4x2 blocks of
 // 32x32 fp32 accumulators (128 per lane).
 //
@@ -16,12 +16,13 @@
 //     matrix-core rate, but gfx950's FP8 MFMAs drop product bits more than
 //     about 2^13 below the largest product of each block (measured: relative
 //     Frobenius error ~1.4e-5 on N(0,1) data), so it is an opt-in kernel.
-// Two LDS stages of 64 KB (A 32 KB + B 32 KB).  Tiles move global -> LDS
-// with buffer_load_dwordx4 ... lds (no staging registers): each wavefront
+// A ring of LCML_GEMM_STAGES (4) LDS stages of one 64-k step each (A 16 KB +
+// B 16 KB for the 256x256 tile).  Tiles move global -> LDS with
+// buffer_load_dwordx4 ... lds (no staging registers): each wavefront
 // instruction deposits one contiguous 1 KB block, lanes whose offset is out
 // of range (rows >= M, k >= K, panels beyond N) deposit zeros.  While the
-// matrix cores work on stage s the next K step streams into stage s^1; one
-// barrier per K step.
+// matrix cores work on one stage, the next three K steps stream into the
+// others; one barrier per K step.
 //
 // LDS layouts (bank-conflict free for 16-lane groups of ds_read_b128 on the
 // 64-bank gfx950 LDS):
@@ -387,8 +388,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             // column's stores are contiguous.  The column's scale and a
             // row-invariant bias are read once per block (lane c holds column
             // c) and taken per column with v_readlane, so the column loop has
-            // no memory reads besides the staged sums and several stores in
-            // flight; a bias that varies over rows is read per element.
+            // no memory reads besides the staged sums; a bias that varies over
+            // rows is read per element.
             const uint32_t ohw = (uint32_t)(g.cv.OH * g.cv.OW);
             const int64_t colb = n0 + wn * WN * 32 + j * 32;  // first column of this block
             const int ncol = colb < e.N ? (int)(e.N - colb < 32 ? e.N - colb : 32) : 0;
@@ -407,7 +408,9 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                     const uint32_t n = (uint32_t)m / ohw, pix = (uint32_t)m - n * ohw;
                     const int64_t ybase = ((int64_t)n * g.cv.CoutTot + (int64_t)grp * e.N) * ohw + pix;
                     if (inv) {
-#pragma unroll 4
+                        // a rolled loop: v_readlane is convergent, so the
+                        // compiler does not unroll around it; the stores do
+                        // not wait, so several are in flight regardless
                         for (int c = 0; c < ncol; ++c) {
                             const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc_l, c));
                             const float cv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(cv_l, c));
