@@ -18,6 +18,10 @@ public:
     explicit Error(const std::string &msg) : std::runtime_error(msg) {}
 };
 
+// a message without arguments is taken verbatim (a '%' in it is not a
+// conversion)
+inline std::string format(const char *msg) { return msg; }
+
 template <typename... Args>
 inline std::string format(const char *fmt, Args... args) {
     int n = std::snprintf(nullptr, 0, fmt, args...);
