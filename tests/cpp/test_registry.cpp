@@ -95,6 +95,15 @@ int main(int argc, char **argv) {
     CHECK(!opset.has_operator("NotAnOp"));
     Node bogus("n", "NotAnOp");
     CHECK(throws([&] { opset.create_operator("NotAnOp", bogus); }));
+    // error messages: without arguments verbatim ('%' is not a conversion), with arguments formatted
+    CHECK(lcml::onnx::format("x %s 100% %d") == "x %s 100% %d");
+    CHECK(lcml::onnx::format("K=%d of %s", 7, "W") == "K=7 of W");
+    try {
+        LCML_ASSERT(false, "c % 4 != 0");
+        CHECK(false);
+    } catch (const lcml::onnx::Error &e) {
+        CHECK(std::string(e.what()) == "c % 4 != 0");
+    }
 
     // ---- import the reference's fixture graph ----
     Model m = Model::load_from_json(read_text(golden + "/simple_mlp.onnx.json"));
