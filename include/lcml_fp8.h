@@ -181,7 +181,11 @@ LCML_API int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, in
  * of the fused kernel encodes all of x).  Otherwise x must be
  * contiguous (ldx == K) and the call quantises into `workspace`
  * (lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel) bytes) and runs the
- * GEMM selected by `kernel`.
+ * GEMM selected by `kernel`.  The size query assumes a 16-byte aligned x:
+ * where it returns 0 but x is not 16-byte aligned, the call takes the
+ * two-step path and needs lcml_fp8_gemm_dynamic_workspace_bytes(M, K,
+ * LCML_KERNEL_MFMA) bytes (a smaller workspace is rejected before any
+ * launch).
  * x_scale_out: optional device float that receives s.
  * Epilogue arguments and y as for lcml_fp8_gemm.
  * The reference has no dynamic quantiser; this replaces the composition

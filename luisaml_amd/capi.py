@@ -242,7 +242,9 @@ def gemm_dynamic(x: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor,
     ydt = _DTYPE_CODE.get(y.dtype, 0)
     cc, nd, c0, c1 = _c_args(c)
     per_ch = int(b_scale.numel() > 1)
-    need = lib().lcml_fp8_gemm_dynamic_workspace_bytes(M, K, int(kernel))
+    # the size query assumes a 16-byte aligned x; a misaligned x takes the
+    # two-step path, whose size the (never fusing) MFMA kernel's query gives
+    need = lib().lcml_fp8_gemm_dynamic_workspace_bytes(M, K, int(kernel) if x.data_ptr() % 16 == 0 else KERNEL_MFMA)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     ws_bytes = workspace.numel() if workspace is not None else 0

@@ -236,13 +236,14 @@ bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kern
 }
 int64_t pad256(int64_t n) { return (n + 255) / 256 * 256; }
 static_assert(LCML_FP8_DYNAMIC_WORKSPACE_BYTES >= lcml::kMaxAmaxPartials * 4, "workspace holds the partial maxima");
+// quantised activations, the partial maxima, the scale (when not returned)
+int64_t two_step_workspace_bytes(int64_t M, int64_t K) { return pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256; }
 }  // namespace
 
 int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel) {
     if (M <= 0 || K <= 0) return 0;
     if (dynamic_fusable(M, K, nullptr, K, kernel)) return 0;
-    // quantised activations, the partial maxima, the scale (when not returned)
-    return pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256;
+    return two_step_workspace_bytes(M, K);
 }
 
 int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx, const uint8_t *b_packed,
@@ -266,9 +267,12 @@ int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64
         return hip_status(lcml::launch_gemm_skinny_dynamic(M, N, K, x, ldx, b_packed, e, x_scale_out,
                                                            kernel != LCML_KERNEL_SKINNY_FP8, s),
                           fn);
-    // two-step path: quantise into the workspace, then the selected GEMM
+    // two-step path: quantise into the workspace, then the selected GEMM.
+    // The size is that of this path whatever the size query said: the query
+    // cannot see x, and a misaligned x takes this path where an aligned one
+    // would have fused.
     if (ldx != K) return fail(LCML_ERR_UNSUPPORTED, "%s: x must be contiguous (ldx == K) for M=%lld", fn, (long long)M);
-    const int64_t need = lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel);
+    const int64_t need = two_step_workspace_bytes(M, K);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
         return fail(LCML_ERR_INVALID_ARG, "%s: needs a 256-byte aligned workspace of %lld bytes", fn,
                     (long long)need);

@@ -23,6 +23,8 @@ CXX = [HIPCC, "-std=c++20", "-O2", "-fPIC", "-Wall", "-Wno-unused-command-line-a
 DRIVERS = {  # test drivers under tests/cpp
     "test_registry": os.path.join(ROOT, "tests", "cpp", "test_registry.cpp"),
     "test_network": os.path.join(ROOT, "tests", "cpp", "test_network.cpp"),
+    # the FP8 QDQ MLP model-file fixture writer (tests/golden/fp8_mlp.*)
+    "write_fp8_mlp": os.path.join(ROOT, "tests", "golden", "write_fp8_mlp.cpp"),
 }
 
 

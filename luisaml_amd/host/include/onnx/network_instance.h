@@ -74,6 +74,7 @@ class NetworkInstance {
     void create_tensor_for_var(const Variable &var);
     void validate_and_bind(std::string_view role, const Variable &var, ITensor &t);
     void fuse_qdq_linear();
+    bool is_zero_e4m3_constant(const Variable &v) const;
     void pack_weights();
     void plan_intermediates();
 

@@ -204,7 +204,9 @@ public:
     OperatorSet(std::string domain, int64_t version) : domain_(std::move(domain)), version_(version) {}
     const std::string &get_domain() const { return domain_; }
     int64_t get_version() const { return version_; }
-    void register_operator(std::string name, Factory f) { factories_.insert_or_assign(std::move(name), std::move(f)); }
+    // the first registration of a name wins, as the reference's emplace
+    // (include/onnx/onnx.h:358)
+    void register_operator(std::string name, Factory f) { factories_.try_emplace(std::move(name), std::move(f)); }
     std::unique_ptr<Operator> create_operator(std::string_view name, const Node &node) const {
         auto it = factories_.find(std::string(name));
         LCML_ASSERT(it != factories_.end(), "Operator not found: %.*s", (int)name.size(), name.data());
@@ -258,11 +260,31 @@ public:
     int32_t get_ir_version() const { return ir_version_; }
     const std::string &get_producer_name() const { return producer_name_; }
     const std::string &get_producer_version() const { return producer_version_; }
+    // The ONNX-JSON text load_from_json reads back: the reference exporter's
+    // format (snake_case keys, dtype names as strings, integers as strings,
+    // blob initializers as data_offsets, scripts/export_onnx.py:26-173).
+    // Initializers and value_info are written sorted by name, so the text
+    // depends only on the graph.
+    std::string save_to_json() const;
 
     // ONNX-JSON (protobuf JSON mapping) with initializers either base64
     // raw_data or data_offsets into an external weight blob
     // (src/onnx/onnx.cpp:87-125, 190-242 of the reference).
     static Model load_from_json(std::string_view json);
+};
+
+// Builds the external weight blob of a model file: each add() places the
+// bytes at the next 4-byte aligned offset and returns the initializer
+// Variable with its data_offsets.  FP8 tensors (FLOAT8E4M3FN / FLOAT8E5M2)
+// take ((n + 3) / 4) * 4 bytes, zero padded, the size the loader requires
+// of them (src/onnx/network_instance.cpp:222-224); every other type takes
+// n * sizeof(element) bytes.
+class WeightBlobWriter {
+    std::vector<uint8_t> bytes_;
+
+public:
+    Variable add(std::string name, DataType dt, std::vector<size_t> shape, const void *data, size_t nbytes);
+    const std::vector<uint8_t> &bytes() const { return bytes_; }
 };
 
 // Read a scalar/list attribute with a default.

@@ -120,16 +120,23 @@ void NetworkInstance::create_tensor_for_var(const Variable &var) {
 // activation into Conv (4-D E4M3 weight, channels per group % 16 == 0)
 // becomes one FP8Conv node.
 // ------------------------------------------------------------------------
-namespace {
-
-bool is_zero_constant(TensorTable &, const Variable &v) {
-    if (!v.is_constant()) return false;
+// An E4M3 zero point that is a constant holding only 0x00 bytes, embedded
+// (raw_data) or in the weight blob (read back from the device; a zero point
+// is one byte per scale entry, so at most a few KB).  Anything else -- another
+// element type, a non-constant, a nonzero byte -- keeps the node unfused.
+bool NetworkInstance::is_zero_e4m3_constant(const Variable &v) const {
+    if (!v.is_constant() || v.get_dtype() != DataType::FLOAT8E4M3FN) return false;
+    const size_t n = v.num_elements();
+    auto zero = [](const uint8_t *p, size_t k) { return std::all_of(p, p + k, [](uint8_t c) { return c == 0; }); };
     const std::string &raw = v.get_raw_data();
-    if (!raw.empty()) return std::all_of(raw.begin(), raw.end(), [](char c) { return c == 0; });
-    return false;  // zero points in the weight blob are checked when the tensor exists
+    if (!raw.empty()) return raw.size() >= n && zero(reinterpret_cast<const uint8_t *>(raw.data()), n);
+    if (!v.is_trainable_weight() || weight_buffer_ == nullptr) return false;
+    auto [start, end] = v.get_buffer_range();
+    if (end > weight_bytes_ || end - start < n || n > 65536) return false;
+    std::vector<uint8_t> host(n);
+    hip_check(hipMemcpy(host.data(), weight_buffer_ + start, n, hipMemcpyDeviceToHost), "hipMemcpy");
+    return zero(host.data(), n);
 }
-
-}  // namespace
 
 void NetworkInstance::fuse_qdq_linear() {
     Graph &g = model_.mutable_graph();
@@ -165,16 +172,19 @@ void NetworkInstance::fuse_qdq_linear() {
         const Node *dqa = prod(A.get_name());
         if (!dqa || dqa->get_op_type() != "DequantizeLinear" || !only_consumer(A.get_name(), who)) return r;
         const Variable &qv = dqa->get_inputs()[0].get();
+        // the fused kernels quantise to E4M3: an E5M2 or integer Q -> DQ stays
+        // op by op (its own QuantizeLinear / DequantizeLinear semantics)
+        if (qv.get_dtype() != DataType::FLOAT8E4M3FN) return r;
         const Node *q = prod(qv.get_name());
         // the DQ zero point is a constant 0, or DynamicQuantizeLinear's own (zero) output
-        bool zp_ok = dqa->get_inputs().size() <= 2 || is_zero_constant(table_, dqa->get_inputs()[2].get()) ||
+        bool zp_ok = dqa->get_inputs().size() <= 2 || is_zero_e4m3_constant(dqa->get_inputs()[2].get()) ||
                      (q && q->get_op_type() == "DynamicQuantizeLinear" && q->get_outputs().size() > 2 &&
                       &q->get_outputs()[2].get() == &dqa->get_inputs()[2].get());
         if (!q || !zp_ok || !only_consumer(qv.get_name(), prod_idx(A.get_name())) ||
             dqa->get_inputs()[1].get().num_elements() != 1)
             return r;
         if (q->get_op_type() == "QuantizeLinear" && &q->get_inputs()[1].get() == &dqa->get_inputs()[1].get() &&
-            (q->get_inputs().size() <= 2 || is_zero_constant(table_, q->get_inputs()[2].get())) &&
+            (q->get_inputs().size() <= 2 || is_zero_e4m3_constant(q->get_inputs()[2].get())) &&
             attr_int(*q, "saturate", 1) == 1) {
             r.a_mode = 1;
             r.src = &q->get_inputs()[0].get();
@@ -222,7 +232,7 @@ void NetworkInstance::fuse_qdq_linear() {
         if (W.get_dtype() != DataType::FLOAT8E4M3FN || !W.is_constant() || W.get_shape().size() != rank)
             return nullptr;
         if (!dqw->get_inputs()[1].get().is_constant()) return nullptr;
-        if (dqw->get_inputs().size() > 2 && !is_zero_constant(table_, dqw->get_inputs()[2].get())) return nullptr;
+        if (dqw->get_inputs().size() > 2 && !is_zero_e4m3_constant(dqw->get_inputs()[2].get())) return nullptr;
         return dqw;
     };
 
@@ -232,26 +242,31 @@ void NetworkInstance::fuse_qdq_linear() {
         const Node &n = nodes[i];
         if (n.get_op_type() == "Conv") {
             // ---- DQ(x) , DQ(W_e4m3 [cout, cin, kh, kw]) -> Conv [-> act] ----
+            // 2-D, or 1-D as a 1 x kl kernel over [n, c, 1, l]; auto_pad is
+            // ignored as in the reference (only `pads` enters, conv.cpp:257-275)
             const int group = attr_int(n, "group", 1);
-            if (n.get_inputs().size() < 2 || group < 1 || attr_string(n, "auto_pad", "NOTSET") != "NOTSET") continue;
+            if (n.get_inputs().size() < 2 || group < 1) continue;
             const Variable &X = n.get_inputs()[0].get();
             const Variable &Bv = n.get_inputs()[1].get();
-            const Node *dqw = match_weight(Bv, i, 4);
+            const size_t rank = X.get_shape().size();
+            if (rank != 3 && rank != 4) continue;
+            const Node *dqw = match_weight(Bv, i, rank);
             if (!dqw) continue;
             const Variable &W = dqw->get_inputs()[0].get();
             const Variable &sw = dqw->get_inputs()[1].get();
             const auto &ws = W.get_shape();
-            const size_t cout = ws[0], cin = ws[1], kh = ws[2], kw = ws[3];  // cin: channels per group
+            // cin: channels per group
+            const size_t cout = ws[0], cin = ws[1], kh = rank == 4 ? ws[2] : 1, kw = ws[rank - 1];
             if (cin % 16 != 0 || cout % (size_t)group != 0) continue;
             if (sw.num_elements() != 1 && !(sw.num_elements() == cout && attr_int(*dqw, "axis", 1) == 0)) continue;
-            if (X.get_shape().size() != 4 || X.get_shape()[1] != cin * (size_t)group) continue;
+            if (X.get_shape()[1] != cin * (size_t)group) continue;
             ActQ aq = match_act(X, i);
             if (aq.a_mode == 0) continue;  // FP8 conv needs a quantised activation
             std::vector<size_t> drop = aq.drop;
             drop.push_back(prod_idx(Bv.get_name()));
             const Variable *out = &n.get_outputs()[0].get();
             const int act = match_epilogue(out, drop);
-            std::string pname = W.get_name() + "::packed_conv";
+            std::string pname = W.get_name() + "::packed_conv::" + sw.get_name() + "::g" + std::to_string(group);
             if (!g.has_var(pname)) {
                 Variable pv(pname, DataType::FLOAT8E4M3FN, {kh * kw * cin, cout});
                 pv.set_is_constant(true);
@@ -267,7 +282,8 @@ void NetworkInstance::fuse_qdq_linear() {
             f.add_output(*out);
             for (const char *a : {"strides", "pads", "dilations", "group"})
                 if (auto *at = n.try_get_attr(a)) f.set_attribute(*at);
-            f.set_attribute(Attribute{"kernel_shape", std::vector<int32_t>{(int32_t)kh, (int32_t)kw}});
+            f.set_attribute(Attribute{"kernel_shape", rank == 4 ? std::vector<int32_t>{(int32_t)kh, (int32_t)kw}
+                                                                 : std::vector<int32_t>{(int32_t)kw}});
             f.set_attribute(Attribute{"a_mode", (int32_t)aq.a_mode});
             f.set_attribute(Attribute{"has_bias", (int32_t)has_bias});
             f.set_attribute(Attribute{"act", (int32_t)act});
@@ -279,7 +295,9 @@ void NetworkInstance::fuse_qdq_linear() {
         }
         const bool gemm = n.get_op_type() == "Gemm", matmul = n.get_op_type() == "MatMul";
         if (!gemm && !matmul) continue;
-        if (gemm && attr_int(n, "transA", 0) != 0) continue;
+        // transA = 1 (A is [K, M], gemm.cpp:35-40) fuses with a quantised
+        // activation: the quantiser writes the transposed E4M3 copy
+        const bool trans_a = gemm && attr_int(n, "transA", 0) != 0;
         const Variable &A = n.get_inputs()[0].get();
         const Variable &B = n.get_inputs()[1].get();
         // ---- B = DequantizeLinear(W_e4m3 constant, s_w [, 0]) ----
@@ -297,13 +315,15 @@ void NetworkInstance::fuse_qdq_linear() {
             const int n_axis = w_is_nk ? 0 : 1;
             if (axis != n_axis || nscale != N) continue;  // only per-output-channel scales fuse
         }
-        if (A.get_shape().empty() || A.get_shape().back() != K) continue;
+        if (A.get_shape().empty()) continue;
+        if (trans_a ? (A.get_shape().size() != 2 || A.get_shape()[0] != K) : A.get_shape().back() != K) continue;
         // ---- A: static QDQ, dynamic QDQ, or fp32 ----
         ActQ aq = match_act(A, i);
         // E4M3 activation rows need a 16-byte pitch (K % 16 == 0); otherwise
         // the activation's Q/DQ nodes stay and the fused node runs W8A32 on
         // their (exactly representable) fp32 output
         if (aq.a_mode != 0 && K % 16 != 0) aq = ActQ{0, &A, nullptr, {}};
+        if (trans_a && aq.a_mode == 0) continue;  // W8A32 reads A row-major: stays unfused
         const int a_mode = aq.a_mode;  // 0: fp32 (W8A32), 1: static scale, 2: dynamic per-tensor
         const Variable *a_src = aq.src, *a_scale = aq.scale;
         std::vector<size_t> drop = {prod_idx(B.get_name())};
@@ -313,7 +333,9 @@ void NetworkInstance::fuse_qdq_linear() {
         const Variable *out = &n.get_outputs()[0].get();
         const int act = match_epilogue(out, drop);
         // ---- build the fused node ----
-        std::string pname = W.get_name() + "::packed";
+        // one packed copy per (weight, scale, layout): a weight shared by two
+        // nodes through different DequantizeLinear scales or transB packs twice
+        std::string pname = W.get_name() + "::packed::" + sw.get_name() + (w_is_nk ? "::nk" : "::kn");
         if (!g.has_var(pname)) {
             Variable pv(pname, DataType::FLOAT8E4M3FN, {K, N});
             pv.set_is_constant(true);
@@ -333,6 +355,7 @@ void NetworkInstance::fuse_qdq_linear() {
         f.set_attribute(Attribute{"alpha", gemm ? attr_float(n, "alpha", 1.0f) : 1.0f});
         f.set_attribute(Attribute{"beta", gemm ? attr_float(n, "beta", 1.0f) : 1.0f});
         f.set_attribute(Attribute{"w_is_nk", (int32_t)w_is_nk});
+        f.set_attribute(Attribute{"trans_a", (int32_t)trans_a});
         f.set_attribute(Attribute{"weight", W.get_name()});
         for (size_t d : drop) removed[d] = true;
         replacement.emplace(i, std::move(f));
@@ -363,12 +386,14 @@ void NetworkInstance::pack_weights() {
         const uint32_t K = (uint32_t)pv.get_shape()[0], N = (uint32_t)pv.get_shape()[1];
         const auto &ws = W.get_shape();
         const int64_t group = conv ? attr_int(n, "group", 1) : 1;
-        DeviceArray<uint8_t> packed(conv ? (size_t)lcml_fp8_packed_conv_weight_bytes(ws[0], ws[1], ws[2], ws[3], group)
+        // conv weights [cout, cin_g, kh, kw], or [cout, cin_g, kl] (1-D: kh = 1)
+        const int64_t ckh = conv && ws.size() == 4 ? (int64_t)ws[2] : 1, ckw = conv ? (int64_t)ws.back() : 1;
+        DeviceArray<uint8_t> packed(conv ? (size_t)lcml_fp8_packed_conv_weight_bytes(ws[0], ws[1], ckh, ckw, group)
                                          : (size_t)lcml_fp8_packed_weight_bytes(K, N));
         ITensor &wt = table_.at(W.get_name());
         if (conv)
-            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), ws[0], ws[1], ws[2],
-                                                 ws[3], group, packed.data(), stream_),
+            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), ws[0], ws[1], ckh, ckw,
+                                                 group, packed.data(), stream_),
                        "pack conv weight");
         else
             lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,

@@ -244,14 +244,16 @@ std::string base64_decode(std::string_view in) {
     return out;
 }
 
+// A tensor type without a dim list (how ONNX writes a scalar, e.g. the
+// y_scale / y_zero_point outputs of DynamicQuantizeLinear) has shape [1], as
+// in the reference's Variable::from_json (src/onnx/onnx.cpp:93-95).
 std::vector<size_t> shape_of_type(const JValue &type) {
     std::vector<size_t> shape;
     auto *tt = type.get("tensor_type");
     if (!tt) return shape;
     auto *sh = tt->get("shape");
-    if (!sh) return shape;
-    auto *dims = sh->get("dim");
-    if (!dims) return shape;
+    auto *dims = sh ? sh->get("dim") : nullptr;
+    if (!dims || dims->arr.empty()) return {1};
     for (auto &d : dims->arr) {
         auto *dv = d.get("dim_value");
         LCML_ASSERT(dv, "graph variable with a symbolic dimension (static shapes are required)");
@@ -279,9 +281,8 @@ Variable initializer_from_json(const JValue &j) {
     std::vector<size_t> shape;
     if (auto *dims = j.get("dims")) {
         for (auto &d : dims->arr) shape.push_back((size_t)d.as_int());
-    } else {
-        shape.push_back(1);
     }
+    if (shape.empty()) shape.push_back(1);  // a scalar initializer (onnx.cpp:107-108)
     if (auto *off = j.get("data_offsets")) {
         LCML_ASSERT(off->arr.size() == 2, "initializer %s: data_offsets needs [start, end]", name.c_str());
         return Variable{std::move(name), dt, std::move(shape), {}, (uint64_t)off->arr[0].as_int(),

@@ -134,15 +134,18 @@ public:
 // inputs: [A, W packed, w_scale, (a_scale if a_mode == 1), (C if has_c)]
 // a_mode 0: A fp32, W8A32 kernel; 1: A quantised with the static a_scale;
 // 2: A quantised with its dynamic per-tensor scale (amax/448).
+// trans_a: A is [K, M] (Gemm transA=1); the quantiser writes the [M, K]
+// E4M3 copy as a transposing NCHW -> NHWC quantise of a [1, K, 1, M] view.
 class FP8Linear : public StreamOperator {
-    int a_mode_, has_c_, act_;
+    int a_mode_, has_c_, act_, trans_a_;
     float alpha_, beta_;
-    std::unique_ptr<DeviceBuffer> qa_, ws_;
+    std::unique_ptr<DeviceBuffer> qa_, ws_, sx_;
     size_t qa_bytes_ = 0, ws_bytes_ = 0;
 
 public:
-    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta)
-        : StreamOperator("FP8Linear"), a_mode_(a_mode), has_c_(has_c), act_(act), alpha_(alpha), beta_(beta) {}
+    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta, int trans_a)
+        : StreamOperator("FP8Linear"), a_mode_(a_mode), has_c_(has_c), act_(act), trans_a_(trans_a), alpha_(alpha),
+          beta_(beta) {}
     void forward(std::span<std::reference_wrapper<ITensor>> inputs,
                  std::span<std::reference_wrapper<ITensor>> outputs) override {
         ITensor &A = inputs[0], &Y = outputs[0];
@@ -159,6 +162,35 @@ public:
         CArgs c = c_args(C);
         const int ydt = out_dtype_code(Y, "FP8Linear");
         const float *a = static_cast<const float *>(A.device_data());
+        LCML_ASSERT(!trans_a_ || (a_mode_ != 0 && A.ndim() == 2 && A.shape(0) == K),
+                    "FP8Linear: transA needs a quantised [K, M] activation");
+        if (trans_a_) {
+            const size_t need = (size_t)(M * K);
+            if (!qa_ || qa_bytes_ < need) {
+                qa_ = std::make_unique<DeviceBuffer>(need);
+                qa_bytes_ = need;
+            }
+            uint8_t *q = static_cast<uint8_t *>(qa_->data());
+            const float *sa;
+            if (a_mode_ == 1) {
+                sa = static_cast<const float *>(a_scale->device_data());
+                check(lcml_fp8_quantize_nhwc(a, q, 1, K, 1, M, sa, nullptr, nullptr, stream_), "FP8Linear quantize");
+            } else {
+                if (!sx_) sx_ = std::make_unique<DeviceBuffer>(sizeof(float));
+                if (!ws_ || ws_bytes_ < (size_t)LCML_FP8_DYNAMIC_WORKSPACE_BYTES) {
+                    ws_ = std::make_unique<DeviceBuffer>((size_t)LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
+                    ws_bytes_ = LCML_FP8_DYNAMIC_WORKSPACE_BYTES;
+                }
+                check(lcml_fp8_quantize_nhwc(a, q, 1, K, 1, M, nullptr, static_cast<float *>(sx_->data()), ws_->data(),
+                                             stream_),
+                      "FP8Linear quantize");
+                sa = static_cast<const float *>(sx_->data());
+            }
+            check(lcml_fp8_gemm(M, N, K, q, K, sa, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
+                                c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, LCML_KERNEL_AUTO, stream_),
+                  "FP8Linear");
+            return;
+        }
         if (a_mode_ == 0) {
             check(lcml_fp8_gemm_w8a32(M, N, K, a, K, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
                                       c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, stream_),
@@ -168,7 +200,11 @@ public:
         if (a_mode_ == 2) {
             // DynamicQuantizeLinear -> DQ -> Gemm in one call (one fused launch
             // for small M*K; otherwise quantise into the workspace + GEMM)
-            const int64_t ws = lcml_fp8_gemm_dynamic_workspace_bytes(M, K, LCML_KERNEL_AUTO);
+            // the size query assumes a 16-byte aligned A; a misaligned one
+            // takes the two-step path (the MFMA kernel's size)
+            const bool a16 = (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+            const int64_t ws =
+                lcml_fp8_gemm_dynamic_workspace_bytes(M, K, a16 ? LCML_KERNEL_AUTO : LCML_KERNEL_MFMA);
             if (ws > 0 && (!ws_ || ws_bytes_ < (size_t)ws)) {
                 ws_ = std::make_unique<DeviceBuffer>((size_t)ws);
                 ws_bytes_ = (size_t)ws;
@@ -210,7 +246,7 @@ REGISTER_TO_DEFAULT_OPSET(Gelu) {
 REGISTER_TO_DEFAULT_OPSET(FP8Linear) {
     return std::make_unique<FP8Linear>(attr_int(node, "a_mode", 0), attr_int(node, "has_c", 0),
                                        attr_int(node, "act", 0), attr_float(node, "alpha", 1.0f),
-                                       attr_float(node, "beta", 1.0f));
+                                       attr_float(node, "beta", 1.0f), attr_int(node, "trans_a", 0));
 };
 
 }  // namespace lcml::onnx

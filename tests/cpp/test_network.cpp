@@ -18,7 +18,14 @@
 //  10. Add / Sub / Mul / Div on FLOAT, E4M3 and E5M2 tensors with
 //      broadcasting, and a DynamicQuantizeLinear zero-point output;
 //  11. the device-buffer planner: a 9-node graph run with one planned arena
-//      and with one allocation per intermediate, bit-identical outputs.
+//      and with one allocation per intermediate, bit-identical outputs;
+//  12. the FP8 QDQ MLP model file (tests/golden/fp8_mlp.*) loaded from disk,
+//      fused (3 FP8Linear) and op by op, against its stored oracle output;
+//  13. an E5M2 activation QDQ stays unfused in front of an E4M3 weight;
+//  14. scalar (0-D) value_info of DynamicQuantizeLinear outputs;
+//  15. one E4M3 weight behind two scales and two layouts;
+//  16. Gemm(transA=1) with static and dynamic activation QDQ, fused;
+//  17. 1-D Conv with auto_pad, fp32 and fused FP8.
 //   usage: test_network <tests/golden dir>
 #include <algorithm>
 #include <cmath>
@@ -973,6 +980,331 @@ static void test_fp8_tensor_conv(bool e5m2) {
     CHECK(far == 0 && near * 200 <= y.size());
 }
 
+// Runs `m` on one fp32 input and returns the fp32 output (fusion on or off).
+static std::vector<float> run_model(Model &&m, const void *blob, size_t blob_bytes, const std::string &in,
+                                    const std::vector<float> &x, ITensor::shape_type xs, const std::string &out,
+                                    ITensor::shape_type ys, bool fused, std::vector<std::string> *types = nullptr,
+                                    size_t *fused_count = nullptr) {
+    auto xt = upload(x, xs);
+    auto yt = make_device_tensor<float>(ys);
+    NetworkInstance net;
+    net.set_model(std::move(m));
+    net.set_fusion(fused);
+    if (blob) net.set_weight_buffer(blob, blob_bytes);
+    net.set_input(in, *xt);
+    net.set_output(out, *yt);
+    net.forward();
+    if (types) *types = net.executed_op_types();
+    if (fused_count) *fused_count = net.fused_linear_count();
+    return download<float>(*yt);
+}
+
+static bool all_ops(const std::vector<std::string> &t, const char *op, size_t n) {
+    return t.size() == n && std::all_of(t.begin(), t.end(), [&](const std::string &x) { return x == op; });
+}
+
+// The FP8 QDQ MLP model file written by tests/golden/write_fp8_mlp.cpp
+// (ONNX-JSON + weight blob, E4M3 weights and zero points in the blob, 4-byte
+// padded), loaded from disk and run fused (3 FP8Linear nodes: the blob zero
+// points are recognised as zero) and op by op, against the oracle output
+// stored with it; the tolerance is the MLP's (1e-4 of the last layer's
+// bound on the oracle's own activations, plus 1e-5).
+static void test_fp8_mlp_from_file(const std::string &golden, bool fused) {
+    std::printf("[12] FP8 QDQ MLP model file (fp8_mlp.onnx.json + blob), %s\n", fused ? "fused" : "op by op");
+    std::string blob = read_text(golden + "/fp8_mlp.bin");
+    std::string xin = read_text(golden + "/fp8_mlp_input.bin"), yref = read_text(golden + "/fp8_mlp_output.bin");
+    CHECK(xin.size() == 64 * 784 * 4 && yref.size() == 64 * 10 * 4);
+    Model m = Model::load_from_json(read_text(golden + "/fp8_mlp.onnx.json"));
+    // host-side oracle chain for the bound: weights decoded from the blob
+    const Graph &g = m.get_graph();
+    const int dims[4] = {784, 256, 128, 10};
+    std::vector<float> x(64 * 784), want(64 * 10);
+    std::memcpy(x.data(), xin.data(), xin.size());
+    std::memcpy(want.data(), yref.data(), yref.size());
+    std::vector<float> h = x;
+    std::vector<double> bound;
+    for (int l = 0; l < 3; ++l) {
+        const int K = dims[l], N = dims[l + 1];
+        const std::string L = std::to_string(l);
+        auto [ws, we] = g.get_var("net." + L + ".weight").get_buffer_range();
+        auto [ss, se] = g.get_var("net." + L + ".weight_scale").get_buffer_range();
+        auto [bs, be] = g.get_var("net." + L + ".bias").get_buffer_range();
+        CHECK(we - ws == ((size_t)N * K + 3) / 4 * 4 && ws % 4 == 0 && se - ss == 4 && be - bs == (size_t)N * 4);
+        float sc;
+        std::memcpy(&sc, blob.data() + ss, 4);
+        std::vector<float> wdq((size_t)N * K), b(N), out((size_t)64 * N);
+        orc_dequantize(reinterpret_cast<const uint8_t *>(blob.data() + ws), wdq.data(), 1, 1, (int64_t)wdq.size(), &sc);
+        std::memcpy(b.data(), blob.data() + bs, (size_t)N * 4);
+        if (l == 2) {
+            bound.resize(out.size());
+            orc_gemm_abs_bound(64, N, K, h.data(), 0, wdq.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, bound.data());
+        }
+        orc_gemm(64, N, K, h.data(), 0, wdq.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, l < 2 ? 1 : 0, out.data());
+        h = std::move(out);
+    }
+    CHECK(std::memcmp(h.data(), want.data(), want.size() * 4) == 0);  // the stored output is the oracle's
+    DeviceBuffer wb(blob.size());
+    CHECK(hipMemcpy(wb.data(), blob.data(), blob.size(), hipMemcpyHostToDevice) == hipSuccess);
+    std::vector<std::string> types;
+    size_t nf = 0;
+    auto y = run_model(std::move(m), wb.data(), blob.size(), "input", x, {64, 784}, "output", {64, 10}, fused, &types,
+                       &nf);
+    if (fused) CHECK(nf == 3 && all_ops(types, "FP8Linear", 3));
+    else CHECK(nf == 0 && types.size() == 8);
+    CHECK(close(y, want, bound, 1e-4, 1e-5, "fp8 mlp from file"));
+}
+
+// An E5M2 activation Q -> DQ in front of a DQ(E4M3 weight) Gemm: the fused
+// kernels quantise to E4M3, so the activation pair stays op by op (E5M2
+// codes) and only the weight side fuses (W8A32 on the dequantised E5M2
+// values); the result equals the unfused graph's within the GEMM bound.
+static void test_e5m2_activation_stays_unfused() {
+    std::printf("[13] E5M2 activation QDQ -> Gemm(DQ(E4M3 W)): activation pair not fused\n");
+    const int M = 32, K = 256, N = 96;
+    auto x = normals(131, (size_t)M * K, 1.0f), w = normals(132, (size_t)N * K, 0.05f);
+    float sx = 0.01f, sw = orc_scale_from_amax(orc_amax(w.data(), w.size()));
+    std::vector<uint8_t> qw(w.size()), z8(1, 0);
+    orc_quantize(w.data(), qw.data(), 1, 1, (int64_t)qw.size(), &sw);
+    auto build = [&]() {
+        Graph g("e5m2act");
+        var(g, "x", DataType::FLOAT, {(size_t)M, (size_t)K});
+        raw_var(g, "sx", DataType::FLOAT, {1}, &sx, 4);
+        raw_var(g, "zx", DataType::FLOAT8E5M2, {1}, z8.data(), 1);
+        raw_var(g, "W", DataType::FLOAT8E4M3FN, {(size_t)N, (size_t)K}, qw.data(), qw.size());
+        raw_var(g, "sw", DataType::FLOAT, {1}, &sw, 4);
+        var(g, "xq", DataType::FLOAT8E5M2, {(size_t)M, (size_t)K});
+        var(g, "xd", DataType::FLOAT, {(size_t)M, (size_t)K});
+        var(g, "Wf", DataType::FLOAT, {(size_t)N, (size_t)K});
+        var(g, "y", DataType::FLOAT, {(size_t)M, (size_t)N});
+        node(g, "QuantizeLinear", {"x", "sx", "zx"}, {"xq"});
+        node(g, "DequantizeLinear", {"xq", "sx", "zx"}, {"xd"});
+        node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"});
+        node(g, "Gemm", {"xd", "Wf"}, {"y"}, {Attribute{"transB", (int32_t)1}});
+        g.add_input("x");
+        g.add_output("y");
+        Model m(10, "test", "1");
+        m.set_graph(std::move(g));
+        return m;
+    };
+    std::vector<std::string> types;
+    auto yf = run_model(build(), nullptr, 0, "x", x, {(uint32_t)M, (uint32_t)K}, "y", {(uint32_t)M, (uint32_t)N}, true,
+                        &types);
+    auto yu = run_model(build(), nullptr, 0, "x", x, {(uint32_t)M, (uint32_t)K}, "y", {(uint32_t)M, (uint32_t)N}, false);
+    CHECK(types.size() == 3 && types[0] == "QuantizeLinear" && types[1] == "DequantizeLinear" &&
+          types[2] == "FP8Linear");
+    std::vector<uint8_t> qx(x.size());
+    std::vector<float> A(x.size()), Bw(w.size()), ref((size_t)M * N);
+    orc_quantize_e5m2(x.data(), qx.data(), 1, 1, (int64_t)x.size(), &sx, 1);
+    orc_dequantize_e5m2(qx.data(), A.data(), 1, 1, (int64_t)qx.size(), &sx);
+    orc_dequantize(qw.data(), Bw.data(), 1, 1, (int64_t)qw.size(), &sw);
+    orc_gemm(M, N, K, A.data(), 0, Bw.data(), 1, 1.0f, 0.0f, nullptr, -1, 0, 0, 0, ref.data());
+    std::vector<double> bound(ref.size());
+    orc_gemm_abs_bound(M, N, K, A.data(), 0, Bw.data(), 1, 1.0f, 0.0f, nullptr, -1, 0, 0, bound.data());
+    CHECK(close(yf, ref, bound, 1e-4, 0.0, "e5m2 activation, fused weight"));
+    CHECK(close(yu, ref, bound, 1e-4, 0.0, "e5m2 activation, op by op"));
+}
+
+// A model file whose DynamicQuantizeLinear scale / zero-point outputs are
+// declared as ONNX scalars (value_info without a dim list): they load as
+// shape [1] (the reference's Variable::from_json, onnx.cpp:93-95) and the
+// unfused graph runs through the planned arena.
+static void test_scalar_value_info_unfused() {
+    std::printf("[14] 0-D value_info (DynamicQuantizeLinear outputs) from JSON, unfused\n");
+    const int M = 8, K = 64;
+    auto x = normals(141, (size_t)M * K, 2.0f);
+    const char *json = R"({
+  "graph": {
+    "node": [
+      {"input": ["x"], "output": ["xq", "xs", "xz"], "name": "dq", "op_type": "DynamicQuantizeLinear"},
+      {"input": ["xq", "xs", "xz"], "output": ["y"], "name": "dd", "op_type": "DequantizeLinear"}
+    ],
+    "name": "scalars",
+    "input": [{"name": "x", "type": {"tensor_type": {"elem_type": "FLOAT",
+               "shape": {"dim": [{"dim_value": "8"}, {"dim_value": "64"}]}}}}],
+    "output": [{"name": "y", "type": {"tensor_type": {"elem_type": "FLOAT",
+               "shape": {"dim": [{"dim_value": "8"}, {"dim_value": "64"}]}}}}],
+    "value_info": [
+      {"name": "xq", "type": {"tensor_type": {"elem_type": "FLOAT8E4M3FN",
+               "shape": {"dim": [{"dim_value": "8"}, {"dim_value": "64"}]}}}},
+      {"name": "xs", "type": {"tensor_type": {"elem_type": "FLOAT", "shape": {}}}},
+      {"name": "xz", "type": {"tensor_type": {"elem_type": "FLOAT8E4M3FN"}}}
+    ]
+  }
+})";
+    Model m = Model::load_from_json(json);
+    CHECK(m.get_graph().get_var("xs").get_shape() == std::vector<size_t>{1});
+    CHECK(m.get_graph().get_var("xz").get_shape() == std::vector<size_t>{1});
+    auto y = run_model(std::move(m), nullptr, 0, "x", x, {(uint32_t)M, (uint32_t)K}, "y", {(uint32_t)M, (uint32_t)K},
+                       false);
+    float s = orc_scale_from_amax(orc_amax(x.data(), x.size()));
+    std::vector<uint8_t> q(x.size());
+    std::vector<float> ref(x.size());
+    orc_quantize(x.data(), q.data(), 1, 1, (int64_t)q.size(), &s);
+    orc_dequantize(q.data(), ref.data(), 1, 1, (int64_t)q.size(), &s);
+    CHECK(std::memcmp(y.data(), ref.data(), ref.size() * 4) == 0);
+}
+
+// One E4M3 weight W [64, 64] behind two DequantizeLinear nodes with
+// different scales, feeding Gemm(transB=1) and MatMul (W read as [K, N]):
+// each fused node packs its own (weight, scale, layout) copy.
+static void test_tied_weight_two_layouts() {
+    std::printf("[15] one E4M3 weight, two scales and two layouts\n");
+    const int M = 16, D = 64;
+    auto x = normals(151, (size_t)M * D, 1.0f), w = normals(152, (size_t)D * D, 0.05f);
+    float s1 = orc_scale_from_amax(orc_amax(w.data(), w.size())), s2 = 2.5f * s1;
+    std::vector<uint8_t> qw(w.size());
+    orc_quantize(w.data(), qw.data(), 1, 1, (int64_t)qw.size(), &s1);
+    Graph g("tied");
+    var(g, "x", DataType::FLOAT, {(size_t)M, (size_t)D});
+    raw_var(g, "W", DataType::FLOAT8E4M3FN, {(size_t)D, (size_t)D}, qw.data(), qw.size());
+    raw_var(g, "s1", DataType::FLOAT, {1}, &s1, 4);
+    raw_var(g, "s2", DataType::FLOAT, {1}, &s2, 4);
+    var(g, "W1", DataType::FLOAT, {(size_t)D, (size_t)D});
+    var(g, "W2", DataType::FLOAT, {(size_t)D, (size_t)D});
+    var(g, "h", DataType::FLOAT, {(size_t)M, (size_t)D});
+    var(g, "y", DataType::FLOAT, {(size_t)M, (size_t)D});
+    node(g, "DequantizeLinear", {"W", "s1"}, {"W1"});
+    node(g, "DequantizeLinear", {"W", "s2"}, {"W2"});
+    node(g, "Gemm", {"x", "W1"}, {"h"}, {Attribute{"transB", (int32_t)1}});
+    node(g, "MatMul", {"h", "W2"}, {"y"});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    size_t nf = 0;
+    auto y = run_model(std::move(m), nullptr, 0, "x", x, {(uint32_t)M, (uint32_t)D}, "y", {(uint32_t)M, (uint32_t)D},
+                       true, nullptr, &nf);
+    CHECK(nf == 2);
+    std::vector<float> W1(w.size()), W2(w.size()), h((size_t)M * D), ref((size_t)M * D);
+    orc_dequantize(qw.data(), W1.data(), 1, 1, (int64_t)qw.size(), &s1);
+    orc_dequantize(qw.data(), W2.data(), 1, 1, (int64_t)qw.size(), &s2);
+    orc_gemm(M, D, D, x.data(), 0, W1.data(), 1, 1.0f, 0.0f, nullptr, -1, 0, 0, 0, h.data());
+    orc_gemm(M, D, D, h.data(), 0, W2.data(), 0, 1.0f, 0.0f, nullptr, -1, 0, 0, 0, ref.data());
+    // two chained W8A32 layers: the first layer's error (within 1e-4 of its
+    // bound) propagates, so the second bound sums (|h| + bound_h) |W2|
+    std::vector<double> bound(ref.size()), bound_h(h.size());
+    orc_gemm_abs_bound(M, D, D, x.data(), 0, W1.data(), 1, 1.0f, 0.0f, nullptr, -1, 0, 0, bound_h.data());
+    std::vector<float> ah(h.size()), aw(W2.size());
+    for (size_t i = 0; i < h.size(); ++i) ah[i] = std::fabs(h[i]) + (float)bound_h[i];
+    for (size_t i = 0; i < W2.size(); ++i) aw[i] = std::fabs(W2[i]);
+    orc_gemm_abs_bound(M, D, D, ah.data(), 0, aw.data(), 0, 1.0f, 0.0f, nullptr, -1, 0, 0, bound.data());
+    CHECK(close(y, ref, bound, 1e-4, 1e-6, "tied weight"));
+}
+
+// Gemm(transA=1): A is [K, M]; with a static or dynamic activation QDQ it
+// fuses, the quantiser writing the transposed E4M3 copy.
+static void test_gemm_trans_a(bool dynamic) {
+    std::printf("[16] %s QDQ activation -> Gemm(transA=1, transB=1) fused\n", dynamic ? "dynamic" : "static");
+    const int M = 48, K = 160, N = 80;
+    auto xt = normals(161, (size_t)K * M, 1.0f), w = normals(162, (size_t)N * K, 0.05f), b = normals(163, N, 0.01f);
+    float sx = orc_scale_from_amax(orc_amax(xt.data(), xt.size()));
+    float sw = orc_scale_from_amax(orc_amax(w.data(), w.size()));
+    std::vector<uint8_t> qw(w.size()), qx(xt.size()), z8(1, 0);
+    orc_quantize(w.data(), qw.data(), 1, 1, (int64_t)qw.size(), &sw);
+    orc_quantize(xt.data(), qx.data(), 1, 1, (int64_t)qx.size(), &sx);
+    Graph g("transa");
+    var(g, "x", DataType::FLOAT, {(size_t)K, (size_t)M});
+    raw_var(g, "W", DataType::FLOAT8E4M3FN, {(size_t)N, (size_t)K}, qw.data(), qw.size());
+    raw_var(g, "sw", DataType::FLOAT, {1}, &sw, 4);
+    raw_var(g, "b", DataType::FLOAT, {(size_t)N}, b.data(), N * 4);
+    var(g, "xq", DataType::FLOAT8E4M3FN, {(size_t)K, (size_t)M});
+    var(g, "xd", DataType::FLOAT, {(size_t)K, (size_t)M});
+    var(g, "Wf", DataType::FLOAT, {(size_t)N, (size_t)K});
+    var(g, "y", DataType::FLOAT, {(size_t)M, (size_t)N});
+    if (dynamic) {
+        var(g, "xs", DataType::FLOAT, {1});
+        var(g, "xz", DataType::FLOAT8E4M3FN, {1});
+        node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
+        node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+    } else {
+        raw_var(g, "xs", DataType::FLOAT, {1}, &sx, 4);
+        raw_var(g, "xz", DataType::FLOAT8E4M3FN, {1}, z8.data(), 1);
+        node(g, "QuantizeLinear", {"x", "xs", "xz"}, {"xq"});
+        node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+    }
+    node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"});
+    node(g, "Gemm", {"xd", "Wf", "b"}, {"y"}, {Attribute{"transA", (int32_t)1}, Attribute{"transB", (int32_t)1}});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    std::vector<std::string> types;
+    auto y = run_model(std::move(m), nullptr, 0, "x", xt, {(uint32_t)K, (uint32_t)M}, "y", {(uint32_t)M, (uint32_t)N},
+                       true, &types);
+    CHECK(all_ops(types, "FP8Linear", 1));
+    std::vector<float> A(xt.size()), Bw(w.size()), ref((size_t)M * N);
+    orc_dequantize(qx.data(), A.data(), 1, 1, (int64_t)qx.size(), &sx);
+    orc_dequantize(qw.data(), Bw.data(), 1, 1, (int64_t)qw.size(), &sw);
+    orc_gemm(M, N, K, A.data(), 1, Bw.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, 0, ref.data());
+    std::vector<double> bound(ref.size());
+    orc_gemm_abs_bound(M, N, K, A.data(), 1, Bw.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, bound.data());
+    CHECK(close(y, ref, bound, 1e-4, 0.0, "gemm transA"));
+}
+
+// 1-D Conv (X [n, c, l], W [cout, c, kl], conv.cpp:209-250) with an
+// auto_pad attribute the reference parses and ignores: fp32 op by op, and
+// with a dynamic activation QDQ fused into FP8Conv; both against the
+// oracle's direct conv of the [n, c, 1, l] view.
+static void test_conv1d(bool fused) {
+    std::printf("[17] 1-D Conv (stride 2, pad 2, dilation 1, auto_pad SAME_UPPER ignored), %s\n",
+                fused ? "DQ -> FP8Conv" : "fp32");
+    const int64_t Nb = 2, C = 32, L = 40, CO = 24, KL = 5, S = 2, P = 2, OL = (L + 2 * P - KL) / S + 1;
+    auto x = normals(171, (size_t)(Nb * C * L), 1.0f), w = normals(172, (size_t)(CO * C * KL), 0.05f);
+    auto bias = normals(173, (size_t)CO, 0.01f);
+    float sw = orc_scale_from_amax(orc_amax(w.data(), w.size()));
+    std::vector<uint8_t> qw(w.size());
+    orc_quantize(w.data(), qw.data(), 1, 1, (int64_t)qw.size(), &sw);
+    std::vector<float> wd(w.size());
+    orc_dequantize(qw.data(), wd.data(), 1, 1, (int64_t)qw.size(), &sw);
+    Graph g("conv1d");
+    var(g, "x", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)L});
+    var(g, "y", DataType::FLOAT, {(size_t)Nb, (size_t)CO, (size_t)OL});
+    raw_var(g, "B", DataType::FLOAT, {(size_t)CO}, bias.data(), CO * 4);
+    std::vector<Attribute> attrs = {Attribute{"strides", std::vector<int32_t>{(int32_t)S}},
+                                    Attribute{"pads", std::vector<int32_t>{(int32_t)P, (int32_t)P}},
+                                    Attribute{"auto_pad", std::string("SAME_UPPER")},
+                                    Attribute{"kernel_shape", std::vector<int32_t>{(int32_t)KL}}};
+    std::vector<float> xin = x;
+    if (fused) {
+        raw_var(g, "W", DataType::FLOAT8E4M3FN, {(size_t)CO, (size_t)C, (size_t)KL}, qw.data(), qw.size());
+        raw_var(g, "sw", DataType::FLOAT, {1}, &sw, 4);
+        var(g, "xq", DataType::FLOAT8E4M3FN, {(size_t)Nb, (size_t)C, (size_t)L});
+        var(g, "xs", DataType::FLOAT, {1});
+        var(g, "xz", DataType::FLOAT8E4M3FN, {1});
+        var(g, "xd", DataType::FLOAT, {(size_t)Nb, (size_t)C, (size_t)L});
+        var(g, "Wf", DataType::FLOAT, {(size_t)CO, (size_t)C, (size_t)KL});
+        node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
+        node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+        node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"});
+        node(g, "Conv", {"xd", "Wf", "B"}, {"y"}, attrs);
+        float sx = orc_scale_from_amax(orc_amax(x.data(), x.size()));
+        std::vector<uint8_t> qx(x.size());
+        orc_quantize(x.data(), qx.data(), 1, 1, (int64_t)qx.size(), &sx);
+        orc_dequantize(qx.data(), x.data(), 1, 1, (int64_t)qx.size(), &sx);  // x: the dequantised activation
+    } else {
+        raw_var(g, "W", DataType::FLOAT, {(size_t)CO, (size_t)C, (size_t)KL}, wd.data(), wd.size() * 4);
+        node(g, "Conv", {"x", "W", "B"}, {"y"}, attrs);
+    }
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    std::vector<std::string> types;
+    auto y = run_model(std::move(m), nullptr, 0, "x", xin, {(uint32_t)Nb, (uint32_t)C, (uint32_t)L}, "y",
+                       {(uint32_t)Nb, (uint32_t)CO, (uint32_t)OL}, true, &types);
+    CHECK(fused ? all_ops(types, "FP8Conv", 1) : all_ops(types, "Conv", 1));
+    std::vector<float> ref(y.size()), ax(x.size()), aw(wd.size()), ab(bias.size()), bnd(y.size());
+    orc_conv2d(x.data(), wd.data(), bias.data(), ref.data(), Nb, C, 1, L, CO, 1, KL, 1, S, 0, P, 1, 1, 1, 1, OL,
+               LCML_ACT_NONE);
+    for (size_t i = 0; i < x.size(); ++i) ax[i] = std::fabs(x[i]);
+    for (size_t i = 0; i < wd.size(); ++i) aw[i] = std::fabs(wd[i]);
+    for (size_t i = 0; i < bias.size(); ++i) ab[i] = std::fabs(bias[i]);
+    orc_conv2d(ax.data(), aw.data(), ab.data(), bnd.data(), Nb, C, 1, L, CO, 1, KL, 1, S, 0, P, 1, 1, 1, 1, OL,
+               LCML_ACT_NONE);
+    std::vector<double> bound(bnd.begin(), bnd.end());
+    CHECK(close(y, ref, bound, 1e-4, 0.0, "conv1d"));
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -999,6 +1331,15 @@ int main(int argc, char **argv) {
         test_e5m2_qdq_cast();
         test_elementwise();
         test_memory_planner();
+        test_fp8_mlp_from_file(argv[1], true);
+        test_fp8_mlp_from_file(argv[1], false);
+        test_e5m2_activation_stays_unfused();
+        test_scalar_value_info_unfused();
+        test_tied_weight_two_layouts();
+        test_gemm_trans_a(false);
+        test_gemm_trans_a(true);
+        test_conv1d(false);
+        test_conv1d(true);
         test_errors();
     } catch (const Error &e) {
         std::printf("FAIL: uncaught error: %s\n", e.what());

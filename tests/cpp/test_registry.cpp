@@ -153,6 +153,72 @@ int main(int argc, char **argv) {
         CHECK(v == 1.0f);
     }
 
+    // ---- the FP8 QDQ MLP model file (tests/golden/fp8_mlp.*) ----
+    {
+        const std::string text = read_text(golden + "/fp8_mlp.onnx.json");
+        Model m = Model::load_from_json(text);
+        const Graph &g = m.get_graph();
+        const char *ops[] = {"DequantizeLinear", "Gemm", "Relu", "DequantizeLinear", "Gemm",
+                             "Relu", "DequantizeLinear", "Gemm"};
+        CHECK(g.get_nodes().size() == 8);
+        for (size_t i = 0; i < g.get_nodes().size() && i < 8; ++i) CHECK(g.get_nodes()[i].get_op_type() == ops[i]);
+        const size_t blob = read_text(golden + "/fp8_mlp.bin").size();
+        const size_t K[3] = {784, 256, 128}, N[3] = {256, 128, 10};
+        for (int l = 0; l < 3; ++l) {
+            const std::string L = std::to_string(l);
+            const Variable &w = g.get_var("net." + L + ".weight");
+            const Variable &zp = g.get_var("net." + L + ".weight_zero_point");
+            auto [s0, e0] = w.get_buffer_range();
+            CHECK(w.get_dtype() == DataType::FLOAT8E4M3FN && w.is_constant() && w.is_trainable_weight());
+            CHECK((w.get_shape() == std::vector<size_t>{N[l], K[l]}) && e0 - s0 == (N[l] * K[l] + 3) / 4 * 4);
+            CHECK(s0 % 4 == 0 && e0 <= blob);
+            auto [zs, ze] = zp.get_buffer_range();
+            CHECK(zp.get_dtype() == DataType::FLOAT8E4M3FN && ze - zs == 4 && zs % 4 == 0);  // one byte, 4-byte padded
+        }
+        CHECK(g.get_inputs().size() == 1 && g.get_inputs()[0].get().get_name() == "input");
+        CHECK(g.get_outputs().size() == 1 && g.get_outputs()[0].get().get_name() == "output");
+        // the writer is the loader's inverse: the file reproduces byte for byte
+        CHECK(m.save_to_json() == text);
+        // and a weight blob writer pads FP8 ranges to 4 bytes at 4-byte offsets
+        WeightBlobWriter wb;
+        uint8_t five[5] = {1, 2, 3, 4, 5};
+        float f = 2.0f;
+        Variable a = wb.add("a", DataType::FLOAT8E4M3FN, {5}, five, 5);
+        Variable b = wb.add("b", DataType::FLOAT, {1}, &f, 4);
+        Variable c = wb.add("c", DataType::FLOAT8E5M2, {1}, five, 1);
+        CHECK((a.get_buffer_range() == std::pair<uint64_t, uint64_t>{0, 8}));
+        CHECK((b.get_buffer_range() == std::pair<uint64_t, uint64_t>{8, 12}));
+        CHECK((c.get_buffer_range() == std::pair<uint64_t, uint64_t>{12, 16}));
+        CHECK(wb.bytes().size() == 16 && wb.bytes()[5] == 0 && wb.bytes()[4] == 5);
+        CHECK(throws([&] { wb.add("d", DataType::FLOAT, {3}, &f, 4); }));  // size does not match the shape
+    }
+
+    // ---- a scalar value_info (no dim list) loads as shape [1] ----
+    {
+        Model m = Model::load_from_json(R"({"graph": {"node": [
+            {"input": ["x"], "output": ["q", "s", "z"], "op_type": "DynamicQuantizeLinear"}],
+            "input": [{"name": "x", "type": {"tensor_type": {"elem_type": "FLOAT",
+                       "shape": {"dim": [{"dim_value": "4"}]}}}}],
+            "output": [{"name": "s", "type": {"tensor_type": {"elem_type": "FLOAT", "shape": {}}}}],
+            "value_info": [{"name": "z", "type": {"tensor_type": {"elem_type": "FLOAT8E4M3FN"}}}]}})");
+        CHECK((m.get_graph().get_var("s").get_shape() == std::vector<size_t>{1}));
+        CHECK((m.get_graph().get_var("z").get_shape() == std::vector<size_t>{1}));
+    }
+
+    // ---- registration keeps the first factory of a name (onnx.h:358) ----
+    {
+        OperatorSet os("test", 1);
+        os.register_operator("Op", [](const Node &) -> std::unique_ptr<Operator> { return nullptr; });
+        bool second = false;
+        os.register_operator("Op", [&](const Node &) -> std::unique_ptr<Operator> {
+            second = true;
+            return nullptr;
+        });
+        Node n("n", "Op");
+        os.create_operator("Op", n);
+        CHECK(!second);
+    }
+
     // ---- tensor API (borrowed storage: no device allocation) ----
     float dummy[24];
     Tensor<float> t({2, 3, 4}, DeviceArray<float>(dummy, 0, 24));

@@ -120,3 +120,27 @@ def test_fp8_data_type_entry_point_validation():
                              None) == capi.ERR_INVALID_ARG  # at most 8 dimensions
     assert L.lcml_fp8_binary(0, E5, None, sh((0, 3)), 2, None, sh((3,)), 1, None, sh((0, 3)), 2,
                              None) == capi.OK  # empty output: no-op
+
+
+def _gemm_dynamic(M, K, x, ldx, ws, ws_bytes, kernel=0, N=64):
+    return capi.lib().lcml_fp8_gemm_dynamic(M, N, K, x, ldx, 0x1000, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                                            0x1000, 1, N, None, ws, ws_bytes, kernel, None)
+
+
+@pytest.mark.parametrize("kernel", [capi.KERNEL_AUTO, capi.KERNEL_SKINNY])
+def test_dynamic_gemm_misaligned_x_needs_the_two_step_workspace(kernel):
+    """A 4-byte-aligned x cannot take the fused kernel, so the call quantises
+    into the workspace: the size query (which assumes an aligned x) says 0
+    here, and the call must reject a workspace smaller than the two-step path
+    writes, before any launch."""
+    L = capi.lib()
+    M, K = 4, 1024
+    assert L.lcml_fp8_gemm_dynamic_workspace_bytes(M, K, kernel) == 0  # aligned x would fuse
+    two_step = L.lcml_fp8_gemm_dynamic_workspace_bytes(M, K, capi.KERNEL_MFMA)
+    assert two_step == (M * K + 255) // 256 * 256 + capi.DYNAMIC_WORKSPACE_BYTES + 256
+    x = 0x100004  # 4-byte aligned only
+    for ws, nbytes in ((None, 0), (0x200000, 256), (0x200000, two_step - 1)):
+        assert _gemm_dynamic(M, K, x, K, ws, nbytes, kernel) == capi.ERR_INVALID_ARG
+        assert "workspace" in capi.last_error()
+    # a misaligned workspace is rejected too
+    assert _gemm_dynamic(M, K, x, K, 0x200010, two_step, kernel) == capi.ERR_INVALID_ARG

@@ -56,9 +56,10 @@ def test_small_m_decode_linear_full(dev, decode_weight, M):
 ROWS = np.array([0, 1, 255, 256, 1023, 2048, 4095, 4096, 5000, 6143, 7777, 8191])
 
 
-def test_gemm_8192_cubed_sampled_rows(dev):
-    """8192^3, A and B from N(0,1) with per-tensor scales amax/448, bf16 out;
-    12 rows (tile edges included) against the oracle over all 8192 columns."""
+@pytest.fixture(scope="module")
+def cube_8192(dev):
+    """8192^3 operands: A and B from N(0,1), per-tensor scales amax/448
+    (checked bit-exact), B packed; the oracle's sampled-row reference."""
     n = 8192
     a = synth.normal(301, (n, n))
     b = synth.normal(302, (n, n))
@@ -67,13 +68,35 @@ def test_gemm_8192_cubed_sampled_rows(dev):
     sa_ref, sb_ref = np.float32(oracle.dynamic_scale(a)), np.float32(oracle.dynamic_scale(b))
     assert float(sa.item()) == sa_ref and float(sb.item()) == sb_ref
     bp = capi.pack_weight(qb, w_is_nk=False)
-    y = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.float32, kernel=capi.KERNEL_MFMA)
-    ys = y[torch.from_numpy(ROWS).to(dev)].cpu().numpy()
     qa_rows = qa[torch.from_numpy(ROWS).to(dev)].cpu().numpy()
     assert np.array_equal(qa_rows, oracle.quantize(a[ROWS], sa_ref))
-    qb_h = qb.cpu().numpy()
-    ref, A, B = oracle.qlinear(qa_rows, sa_ref, qb_h, sb_ref)
-    assert_close(ys, ref, oracle.gemm_abs_bound(A, B))
+    ref, A, B = oracle.qlinear(qa_rows, sa_ref, qb.cpu().numpy(), sb_ref)
+    del a, b, qb
+    return qa, sa, bp, sb, ref, oracle.gemm_abs_bound(A, B)
+
+
+def test_gemm_8192_cubed_sampled_rows(dev, cube_8192):
+    """8192^3 with the default (exact) tile kernel: 12 rows (tile edges
+    included) against the oracle over all 8192 columns; the bf16 output is
+    the round-to-nearest-even of the fp32 one everywhere."""
+    qa, sa, bp, sb, ref, bound = cube_8192
+    n = 8192
+    y = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.float32, kernel=capi.KERNEL_MFMA)
+    assert_close(y[torch.from_numpy(ROWS).to(dev)].cpu().numpy(), ref, bound)
+    y16 = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.bfloat16, kernel=capi.KERNEL_MFMA)
+    assert torch.equal(y16.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
+
+
+def test_gemm_8192_cubed_native_fp8_sampled_rows(dev, cube_8192):
+    """The native-FP8-MFMA tile kernel (the opt-in fast kernel) at 8192^3:
+    inside the elementwise bound 1e-4 * sum|a*b| and below its documented
+    relative Frobenius error of 3e-5 (gfx950 FP8 MFMA block truncation)."""
+    qa, sa, bp, sb, ref, bound = cube_8192
+    y = capi.gemm(qa, sa, bp, sb, 8192, 8192, out_dtype=torch.float32, kernel=capi.KERNEL_MFMA_FP8)
+    ys = y[torch.from_numpy(ROWS).to(dev)].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(ys - ref) <= 1e-4 * bound)
+    rel = np.linalg.norm(ys - ref) / np.linalg.norm(ref)
+    assert rel < 3e-5, rel
 
 
 def test_transformer_up_projection_gelu_sampled_rows(dev):
@@ -90,6 +113,58 @@ def test_transformer_up_projection_gelu_sampled_rows(dev):
     ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw, bias=bias, act=oracle.ACT_GELU_ERF)
     assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias),
                  act=oracle.ACT_GELU_ERF)
+
+
+@pytest.fixture(scope="module")
+def block_input(dev):
+    """The transformer block's activation x [4096, 4096] fp32 N(0,1), its
+    dynamic scale (bit-exact against the oracle) and sampled rows."""
+    x = synth.normal(420, (4096, 4096))
+    return x, np.float32(oracle.dynamic_scale(x)), ROWS[ROWS < 4096]
+
+
+def block_weight(i, K, N, dev):
+    w = synth.normal(400 + i, (K, N), std=0.02)
+    return per_channel_weight(w, dev) + (synth.normal(410 + i, (N,), std=0.01),)
+
+
+@pytest.mark.parametrize("name,i,N", [("qkv", 0, 12288), ("o", 1, 4096)])
+def test_transformer_qkv_and_o_projection_sampled_rows(dev, block_input, name, i, N):
+    """QKV 4096 -> 12288 and O 4096 -> 4096 at M = 4096 (dynamic activation
+    scale, per-channel weights, fp32 bias): the fp32 output on 12 sampled rows
+    against the oracle; the bf16 output the block uses is the
+    round-to-nearest-even of the fp32 output on every element."""
+    x, s_ref, rows = block_input
+    qw, sw, bp, d_sw, bias = block_weight(i, 4096, N, dev)
+    d_x, d_b = to_dev(x, dev), to_dev(bias, dev)
+    s_out = torch.empty(1, device=dev)
+    y = capi.gemm_dynamic(d_x, bp, d_sw, N, 4096, c=d_b, out_dtype=torch.float32, scale_out=s_out)
+    assert s_out.cpu().numpy().view(np.uint32)[0] == s_ref.view(np.uint32)
+    ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw, bias=bias)
+    assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias))
+    y16 = capi.gemm_dynamic(d_x, bp, d_sw, N, 4096, c=d_b, out_dtype=torch.bfloat16)
+    assert torch.equal(y16.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
+
+
+def test_transformer_down_projection_from_gelu_output(dev, block_input):
+    """Up 4096 -> 11008 + GELU (fp32 out), then down 11008 -> 4096 on that
+    output: the down projection re-quantises the GELU output per tensor
+    through the two-launch workspace path (amax partials + encode, then the
+    tile kernel over K = 11008).  The scale is bit-exact against the oracle's
+    amax/448 over the whole GPU up-projection output, the sampled rows' codes
+    feed the oracle's Gemm."""
+    x, s_ref, rows = block_input
+    _, _, bp_up, d_sw_up, b_up = block_weight(2, 4096, 11008, dev)
+    qw, sw, bp, d_sw, bias = block_weight(3, 11008, 4096, dev)
+    h = capi.gemm_dynamic(to_dev(x, dev), bp_up, d_sw_up, 11008, 4096, c=to_dev(b_up, dev), act=capi.ACT_GELU_ERF)
+    assert capi.lib().lcml_fp8_gemm_dynamic_workspace_bytes(4096, 11008, capi.KERNEL_AUTO) > 0  # two-step path
+    s_out = torch.empty(1, device=dev)
+    y = capi.gemm_dynamic(h, bp, d_sw, 4096, 11008, c=to_dev(bias, dev), out_dtype=torch.float32, scale_out=s_out)
+    h_host = h.cpu().numpy()
+    sh_ref = np.float32(oracle.dynamic_scale(h_host))
+    assert s_out.cpu().numpy().view(np.uint32)[0] == sh_ref.view(np.uint32)
+    ref, A, B = oracle.qlinear(oracle.quantize(h_host[rows], sh_ref), sh_ref, qw, sw, bias=bias)
+    assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias))
 
 
 def test_conv3x3_resnet_one_image(dev):

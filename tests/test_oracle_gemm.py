@@ -129,9 +129,20 @@ def test_gelu_against_exact_erf():
     assert np.array_equal(relu, np.maximum(x, 0))
 
 
-def _im2col_conv(X, W, bias, stride, pad, dil):
+def _im2col_conv(X, W, bias, stride, pad, dil, group=1):
+    """Conv as one GEMM over im2col columns in float64.  With groups the
+    weight matrix is block diagonal: output channel m (group m // (M/group))
+    sees only its group's Cg input channels (conv.cpp:139,158), zeros
+    elsewhere -- an arithmetic independent of the oracle's group loop."""
     N, C, H, Wd = X.shape
     M, Cg, kH, kW = W.shape
+    assert Cg * group == C and M % group == 0
+    Wfull = np.zeros((M, C, kH, kW), np.float64)
+    Mg = M // group
+    for m in range(M):
+        g = m // Mg
+        Wfull[m, g * Cg:(g + 1) * Cg] = W[m]
+    W = Wfull
     oH = (H + 2 * pad - dil * (kH - 1) - 1) // stride + 1
     oW = (Wd + 2 * pad - dil * (kW - 1) - 1) // stride + 1
     Xp = np.zeros((N, C, H + 2 * pad, Wd + 2 * pad), np.float64)
@@ -157,3 +168,23 @@ def test_conv_against_im2col(stride, pad, dil):
     want = _im2col_conv(X, W, b, stride, pad, dil)
     assert got.shape == want.shape
     assert np.max(np.abs(got - want)) < 1e-4
+
+
+@pytest.mark.parametrize("group,stride,pad,dil", [(2, 1, 1, 1), (4, 2, 1, 1), (8, 1, 2, 2), (3, 1, 0, 1)])
+def test_grouped_conv_against_block_diagonal_im2col(group, stride, pad, dil):
+    """The oracle's grouped conv (group g reads input channels g*Cg.. and
+    writes output channels g*M/group.., conv.cpp:139,158) against im2col with
+    a block-diagonal weight; depthwise (group = C = M) included."""
+    C = 24 if group == 3 else 8
+    M = 12 if group == 3 else 8
+    X = synth.normal(11 + group, (2, C, 9, 11))
+    W = synth.normal(12 + group, (M, C // group, 3, 3), std=0.2)
+    b = synth.normal(13 + group, (M,), std=0.1)
+    got = oracle.conv2d(X, W, b, strides=(stride, stride), pads=(pad, pad), dilations=(dil, dil), group=group)
+    want = _im2col_conv(X, W, b, stride, pad, dil, group=group)
+    assert got.shape == want.shape
+    assert np.max(np.abs(got - want)) < 1e-4
+    # a plausible slip (every group reading group 0's channels) is caught
+    if group > 1:
+        wrong = _im2col_conv(X[:, :C // group].repeat(group, axis=1), W, b, stride, pad, dil, group=group)
+        assert np.max(np.abs(got - wrong)) > 1e-2
