@@ -200,6 +200,29 @@ LCML_API int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float 
                           void *workspace, int64_t workspace_bytes, int kernel, void *stream);
 
 /*
+ * lcml_fp8_gemm_dynamic without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid allocation, harnesses that count allocations).  No counterpart
+ * in the reference.  Same arguments, semantics and results (bit for bit) as
+ * lcml_fp8_gemm_dynamic with the workspace arguments removed; where that call
+ * would use its workspace (the two-step quantise + GEMM path), this one uses
+ * a device array of LCML_FP8_NOALLOC_SCRATCH_BYTES that the library holds on
+ * each device it runs on, from the library's load until the process ends.
+ * M * K above LCML_FP8_NOALLOC_MAX_ELEMS is rejected with
+ * LCML_ERR_UNSUPPORTED before anything runs.  The call allocates nothing and
+ * needs no clearing of the array (every byte it reads there it wrote first
+ * in the same call); calls that overlap on one device share the array and
+ * race, so issue them on one stream (or order them) per device.
+ */
+#define LCML_FP8_NOALLOC_MAX_ELEMS 16777216
+#define LCML_FP8_NOALLOC_SCRATCH_BYTES (LCML_FP8_NOALLOC_MAX_ELEMS + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256)
+LCML_API int lcml_fp8_gemm_dynamic_noalloc(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                                           const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel,
+                                           float alpha, const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1,
+                                           float beta, int act, void *y, int y_dtype, int64_t ldy,
+                                           float *x_scale_out, int kernel, void *stream);
+
+/*
  * QuantizeLinear of an NCHW fp32 activation [n, c, h, w] with one per-tensor
  * scale, written in NHWC order (y[n][h][w][c], E4M3) for lcml_fp8_conv2d.
  * y_scale: device float; NULL selects the dynamic scale amax/448 (1 when

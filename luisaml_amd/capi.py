@@ -51,6 +51,8 @@ _SIGS = {
     "lcml_fp8_gemm_dynamic_workspace_bytes": (_i64, [_i64, _i64, _int]),
     "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
                                      _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
+    "lcml_fp8_gemm_dynamic_noalloc": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64,
+                                             _i64, _f32, _int, _vp, _int, _i64, _vp, _int, _vp]),
     "lcml_fp8_quantize_nhwc": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "lcml_fp8_cast": (_int, [_vp, _int, _vp, _int, _i64, _vp]),
     "lcml_fp8_quantize_e5m2": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),

@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "../../include/lcml_fp8.h"
 #include "lcml_internal.hpp"
 
@@ -246,11 +248,16 @@ int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel) 
     return two_step_workspace_bytes(M, K);
 }
 
-int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx, const uint8_t *b_packed,
-                          const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
-                          int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
-                          float *x_scale_out, void *workspace, int64_t workspace_bytes, int kernel, void *stream) {
-    const char *fn = "lcml_fp8_gemm_dynamic";
+}  // extern "C"
+
+namespace {
+// lcml_fp8_gemm_dynamic with the workspace resolved by the caller: the
+// caller's buffer, or the no-allocation entry point's device array.
+int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                      const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
+                      const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
+                      int y_dtype, int64_t ldy, float *x_scale_out, void *workspace, int64_t workspace_bytes,
+                      int kernel, void *stream) {
     if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
                                                (long long)M, (long long)N, (long long)K);
     lcml::Epilogue e;
@@ -284,6 +291,67 @@ int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64
     if (err != hipSuccess) return hip_status(err, fn);
     return lcml_fp8_gemm(M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
                          c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
+}
+
+// The no-allocation variant's workspace: one array per device, in device
+// memory from the moment the library's code object is loaded on that device
+// until the process ends.  `scratch` names a host-side shadow of it; its
+// device address comes from hipGetSymbolAddress, resolved once per device
+// (with that device current) and kept in scratch_addr.  Calls that overlap
+// on one device share it and race.
+constexpr int64_t kNoAllocScratchBytes = LCML_FP8_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoAllocScratchBytes >= LCML_FP8_NOALLOC_MAX_ELEMS + LCML_FP8_DYNAMIC_WORKSPACE_BYTES + 256,
+              "scratch holds the two-step workspace of the largest accepted M*K");
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::atomic<void *> scratch_addr[kMaxDevices];
+
+int noalloc_scratch(const char *fn, void **out) {
+    int dev = 0;
+    if (hipError_t err = hipGetDevice(&dev); err != hipSuccess) return hip_status(err, fn);
+    if (dev < 0 || dev >= kMaxDevices) return fail(LCML_ERR_UNSUPPORTED, "%s: device %d (at most %d)", fn, dev, kMaxDevices);
+    void *p = scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        // the same address on every call: threads racing here store equal values
+        if (hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); err != hipSuccess)
+            return hip_status(err, fn);
+        if (!p) return fail(LCML_ERR_HIP, "%s: no device address for the scratch array", fn);
+        scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return LCML_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx, const uint8_t *b_packed,
+                          const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
+                          int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                          float *x_scale_out, void *workspace, int64_t workspace_bytes, int kernel, void *stream) {
+    return gemm_dynamic_impl("lcml_fp8_gemm_dynamic", M, N, K, x, ldx, b_packed, b_scale, b_scale_per_channel, alpha,
+                             c, c_ndim, c_dim0, c_dim1, beta, act, y, y_dtype, ldy, x_scale_out, workspace,
+                             workspace_bytes, kernel, stream);
+}
+
+int lcml_fp8_gemm_dynamic_noalloc(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                                  const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
+                                  const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act,
+                                  void *y, int y_dtype, int64_t ldy, float *x_scale_out, int kernel, void *stream) {
+    const char *fn = "lcml_fp8_gemm_dynamic_noalloc";
+    if (M > 0 && K > 0 && M * K > LCML_FP8_NOALLOC_MAX_ELEMS)
+        return fail(LCML_ERR_UNSUPPORTED, "%s: M*K=%lld exceeds the no-allocation limit of %lld elements", fn,
+                    (long long)(M * K), (long long)LCML_FP8_NOALLOC_MAX_ELEMS);
+    if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
+                                               (long long)M, (long long)N, (long long)K);
+    if (M == 0) return gemm_dynamic_impl(fn, M, N, K, x, ldx, b_packed, b_scale, b_scale_per_channel, alpha, c,
+                                         c_ndim, c_dim0, c_dim1, beta, act, y, y_dtype, ldy, x_scale_out, nullptr, 0,
+                                         kernel, stream);
+    void *ws = nullptr;
+    if (int rc = noalloc_scratch(fn, &ws)) return rc;
+    return gemm_dynamic_impl(fn, M, N, K, x, ldx, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                             c_dim1, beta, act, y, y_dtype, ldy, x_scale_out, ws, kNoAllocScratchBytes, kernel,
+                             stream);
 }
 
 int lcml_fp8_quantize_nhwc(const float *x, uint8_t *y, int64_t n, int64_t c, int64_t h, int64_t w,

@@ -144,3 +144,20 @@ def test_dynamic_gemm_misaligned_x_needs_the_two_step_workspace(kernel):
         assert "workspace" in capi.last_error()
     # a misaligned workspace is rejected too
     assert _gemm_dynamic(M, K, x, K, 0x200010, two_step, kernel) == capi.ERR_INVALID_ARG
+
+
+def test_noalloc_dynamic_gemm_rejects_oversize_before_any_launch():
+    """The no-allocation entry point refuses M*K above its scratch limit with
+    LCML_ERR_UNSUPPORTED (no device is touched: this runs without a GPU)."""
+    L = capi.lib()
+    limit = header_define("LCML_FP8_NOALLOC_MAX_ELEMS")
+    assert limit == 16 << 20
+    K = 4096
+    M = limit // K + 1
+    rc = L.lcml_fp8_gemm_dynamic_noalloc(M, 64, K, 0x1000, K, 0x1000, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                                         0x1000, 1, 64, None, 0, None)
+    assert rc == capi.ERR_UNSUPPORTED
+    assert "no-allocation limit" in capi.last_error()
+    # M == 0: nothing to do, no scratch needed
+    assert L.lcml_fp8_gemm_dynamic_noalloc(0, 64, K, None, K, None, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                                           0x1000, 1, 64, None, 0, None) == capi.OK
