@@ -5,11 +5,15 @@ Workloads (synthetic data, seeded host generator luisaml_amd.synth):
   * small-M decode linear (the headline line): x[M,4096] fp32 N(0,1) with
     M in {1,4,16}, dynamically QuantizeLinear'd to E4M3 per tensor, times a
     4096x11008 E4M3 weight (N(0,0.02), per-output-channel fp32 scales), bf16
-    out.  One step = the three linears, each = dynamic quantize kernel + GEMM
-    kernel.  Seven distinct copies of the packed weight (315 MB, more than the
-    256 MB MALL) are rotated so that every launch streams its weights from HBM.
+    out.  One step = the three linears, each one lcml_fp8_gemm_dynamic call.
+    Ten distinct copies of the packed weight (451 MB, 1.76x the 256 MB MALL)
+    are rotated so that every launch streams its weights from HBM.
   * 8192^3 GEMM: A, B E4M3 quantised from N(0,1) with per-tensor scales
     (amax/448), fp32 accumulate, bf16 out, fused scalar dequant scale.
+  * transformer-block linears (M = 4096), the ResNet 3x3 conv as an
+    implicit-im2col GEMM, and the 3-layer W8A32 MLP, as sub-lines.
+  * the CPU baseline: the oracle (the reference's arithmetic restated in C)
+    on the host cores, on bounded samples of each workload.
 
 Prints ONE JSON line.  `value` is the small-M whole-step throughput (GB/s of
 algorithmic bytes with inputs resident in HBM); the 8192^3 GEMM TFLOP/s and
@@ -32,7 +36,7 @@ BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA (the exact kernel's instruction
 SMALL_K, SMALL_N, SMALL_MS = 4096, 11008, (1, 4, 16)
 MEDIUM_MS = (32, 64, 128, 256)  # the same linear past decode sizes (a sub-benchmark, not the value)
 BIG = 8192
-N_WEIGHT_COPIES = 7
+N_WEIGHT_COPIES = 10
 
 
 def channel_scales_np(w: np.ndarray, axis: int) -> np.ndarray:
@@ -93,6 +97,8 @@ def main() -> int:
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3",
            "data": "synthetic (seeded splitmix64 + Box-Muller, random-init weights)"}
+
+    cpu_in = {}  # host copies of each workload's operands for the CPU leg
 
     # ------------------------------------------------------------ small-M --
     K, N = SMALL_K, SMALL_N
@@ -244,6 +250,26 @@ def main() -> int:
     })
     del g_steps, g_gemm, g_two
 
+    # HBM read floor: a kernel that only reads the same packed weight bytes
+    # (lcml_fp8_stream_read), rotated over the same copies, back to back in a
+    # graph like the GEMM launches; best over a few grid sizes
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    floor = {}
+    for wgs in (172, 256, 512, 1024, 2048):
+        gf = capture(lambda i, wgs=wgs: capi.stream_read(packed[i % N_WEIGHT_COPIES], sink, wgs), 3 * args.steps)
+        gf.replay()
+        floor[str(wgs)] = round(1e3 * timed(gf.replay) / (3 * args.steps), 2)
+        del gf
+    wbytes = packed[0].numel()
+    best_wgs = min(floor, key=floor.get)
+    out["read_floor"] = {
+        "workload": f"read-only stream of one packed weight copy ({wbytes} B), {N_WEIGHT_COPIES} copies rotated, "
+                    "graph of back-to-back launches; the best a kernel that only reads these bytes achieves",
+        "avg_launch_us_by_workgroups": floor, "best_us": floor[best_wgs],
+        "best_gbs": round(wbytes / (floor[best_wgs] * 1e-6) / 1e9, 1),
+        "frac_hbm": round(wbytes / (floor[best_wgs] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "gemm_over_floor": {m: round(per_launch[m] / floor[best_wgs], 3) for m in per_launch}}
+
     # same-box yardstick: the vendor library (hipBLASLt through torch) on the
     # same small-M shape, E4M3 activations already quantised, per-tensor
     # scales, bf16 out, the same seven rotated weight copies
@@ -367,13 +393,17 @@ def main() -> int:
         Mt, H = 4096, 4096
         shapes = {"qkv": (H, 3 * H), "o": (H, H), "up": (H, 11008), "down": (11008, H)}
         wts = {}
+        cpu_in["transformer"] = {"x": synth.normal(420, (Mt, H)), "shapes": shapes, "w": {}}
         for i, (name, (kk, nn)) in enumerate(shapes.items()):
             wf = torch.from_numpy(synth.normal(400 + i, (kk, nn), std=0.02)).to(dev)
             sc = torch.from_numpy(channel_scales_np(wf.cpu().numpy(), axis=0)).to(dev)
-            wts[name] = (capi.pack_weight(capi.quantize(wf, sc, axis=1), w_is_nk=False), sc,
-                         torch.from_numpy(synth.normal(410 + i, (nn,), std=0.01)).to(dev))
-            del wf
-        xt = torch.from_numpy(synth.normal(420, (Mt, H))).to(dev)
+            qd = capi.quantize(wf, sc, axis=1)
+            bias_h = synth.normal(410 + i, (nn,), std=0.01)
+            wts[name] = (capi.pack_weight(qd, w_is_nk=False), sc, torch.from_numpy(bias_h).to(dev))
+            if not args.no_cpu:  # the same E4M3 codes and scales for the CPU leg
+                cpu_in["transformer"]["w"][name] = (qd.cpu().numpy(), sc.cpu().numpy(), bias_h)
+            del wf, qd
+        xt = torch.from_numpy(cpu_in["transformer"]["x"]).to(dev)
         y_qkv = torch.empty((Mt, 3 * H), dtype=torch.bfloat16, device=dev)
         y_o = torch.empty((Mt, H), dtype=torch.bfloat16, device=dev)
         y_up = torch.empty((Mt, 11008), dtype=torch.float32, device=dev)
@@ -422,7 +452,10 @@ def main() -> int:
         d_wsc = torch.from_numpy(wsc).to(dev)
         qwc = capi.quantize(torch.from_numpy(wc.reshape(cco, -1)).to(dev), d_wsc, axis=0).reshape(cco, cc, 3, 3)
         bpc = capi.pack_conv_weight(qwc.contiguous())
-        bc = torch.from_numpy(synth.normal(602, (cco,), std=0.01)).to(dev)
+        bc_h = synth.normal(602, (cco,), std=0.01)
+        bc = torch.from_numpy(bc_h).to(dev)
+        if not args.no_cpu:
+            cpu_in["conv"] = {"x": xc.cpu().numpy(), "qw": qwc.cpu().numpy(), "sw": wsc, "bias": bc_h}
         xq = torch.empty((cn, ch, cw, cc), dtype=torch.uint8, device=dev)
         sxc = torch.empty(1, dtype=torch.float32, device=dev)
         wsq = torch.empty(256, dtype=torch.uint8, device=dev)
@@ -460,14 +493,16 @@ def main() -> int:
     # 784->256 (+ReLU) -> 128 (+ReLU) -> 10, batch 64, fp32 activations, E4M3
     # weights with one per-tensor scale each through DequantizeLinear (W8A32)
     mlp = []
+    cpu_in["mlp"] = {"x": synth.uniform(520, (64, 784)), "layers": []}
     for i, (kk, nn) in enumerate(((784, 256), (256, 128), (128, 10))):
         wf = synth.normal(500 + i, (nn, kk), std=0.05)  # Gemm transB=1 layout
         sc = np.array([oracle_free_dynamic_scale(wf)], np.float32)
         d_sc = torch.from_numpy(sc).to(dev)
         q = capi.quantize(torch.from_numpy(wf).to(dev), d_sc)
-        mlp.append((capi.pack_weight(q, w_is_nk=True), d_sc, torch.from_numpy(synth.normal(510 + i, (nn,), std=0.01))
-                    .to(dev), kk, nn))
-    x_mlp = torch.from_numpy(synth.uniform(520, (64, 784))).to(dev)
+        b_h = synth.normal(510 + i, (nn,), std=0.01)
+        mlp.append((capi.pack_weight(q, w_is_nk=True), d_sc, torch.from_numpy(b_h).to(dev), kk, nn))
+        cpu_in["mlp"]["layers"].append((q.cpu().numpy(), sc, b_h))
+    x_mlp = torch.from_numpy(cpu_in["mlp"]["x"]).to(dev)
     bufs = [torch.empty((64, nn), dtype=torch.float32, device=dev) for (_, _, _, _, nn) in mlp]
 
     def mlp_fwd(_i=0):
@@ -528,8 +563,68 @@ def main() -> int:
                 "gflops": round(2.0 * rows * BIG * BIG / dt / 1e9, 2), "cores": nt,
                 "sample": f"{rows} rows of the 8192^3 GEMM (dequantize + fma-chain Gemm)"}
 
+        cpu_workloads(out["cpu_baseline"], cpu_in, nt)
+
     print(json.dumps(out), flush=True)
     return 0
+
+
+def cpu_workloads(cb: dict, cpu_in: dict, nt: int) -> None:
+    """The oracle (the reference arithmetic: dequantise, then fp32 fma-chain
+    Gemm / direct conv, gemm.cpp:155-162, conv.cpp:143-192) on bounded samples
+    of the MLP, transformer-linear and conv workloads, on the same operands
+    the GPU ran (E4M3 codes and scales copied back from the device)."""
+    import oracle
+    if "mlp" in cpu_in:  # the whole forward pass, batch 64
+        m = cpu_in["mlp"]
+        layers = [(oracle.dequantize(q, sc), b) for q, sc, b in m["layers"]]
+        reps, t = 0, time.perf_counter()
+        while reps < 200 and time.perf_counter() - t < 2.0:
+            h = m["x"]
+            for j, (wd, b) in enumerate(layers):
+                h = oracle.gemm(h, wd, b, transB=1, act=oracle.ACT_RELU if j < 2 else oracle.ACT_NONE)
+            reps += 1
+        us = 1e6 * (time.perf_counter() - t) / reps
+        cb["mlp_784_256_128_10"] = {"us_per_forward": round(us, 1), "cores": nt,
+                                    "gflops": round(2 * 64 * (784 * 256 + 256 * 128 + 128 * 10) / us / 1e3, 2),
+                                    "sample": f"{reps} full forward passes (batch 64, W8A32: fp32 activations, "
+                                              "dequantised E4M3 weights, bias + ReLU)"}
+    if "transformer" in cpu_in:  # 256 rows of each linear
+        tr, rows = cpu_in["transformer"], 256
+        x = tr["x"]
+        flops, t = 0.0, time.perf_counter()
+        sx = oracle.dynamic_scale(x)  # amax over the whole activation, as the GPU does
+        h_in = {"qkv": x, "o": x, "up": x}
+        for name in ("qkv", "o", "up", "down"):
+            qw, sw, b = tr["w"][name]
+            kk, nn = tr["shapes"][name]
+            xin = h_in[name][:rows]
+            s = sx if name != "down" else oracle.dynamic_scale(xin)  # down: scale of the sampled GELU rows
+            y, _, _ = oracle.qlinear(oracle.quantize(xin, s), s, qw, sw, bias=b,
+                                     act=oracle.ACT_GELU_ERF if name == "up" else oracle.ACT_NONE)
+            if name == "up":
+                h_in["down"] = y.astype(np.float32)
+            flops += 2.0 * rows * kk * nn
+        dt = time.perf_counter() - t
+        cb["transformer_linears_m4096_sample"] = {
+            "gflops": round(flops / dt / 1e9, 2), "seconds": round(dt, 2), "cores": nt,
+            "sample": f"{rows} of the 4096 rows of each linear (QKV, O, up+GELU, down): dynamic quantise "
+                      "(amax over the whole input; for down over the sampled GELU rows), dequantise, "
+                      "fma-chain Gemm + bias"}
+    if "conv" in cpu_in:  # 4 images of the batch of 32
+        c, imgs = cpu_in["conv"], 4
+        t = time.perf_counter()
+        s = oracle.dynamic_scale(c["x"])
+        xi = c["x"][:imgs]
+        A = oracle.dequantize(oracle.quantize(xi, s), s)
+        W = oracle.dequantize(c["qw"].reshape(c["qw"].shape[0], -1), c["sw"], axis=0).reshape(c["qw"].shape)
+        oracle.conv2d(A, W, c["bias"], pads=(1, 1), act=oracle.ACT_RELU)
+        dt = time.perf_counter() - t
+        f = 2.0 * imgs * 56 * 56 * 256 * 256 * 9
+        cb["conv3x3_resnet_sample"] = {
+            "gflops": round(f / dt / 1e9, 2), "seconds": round(dt, 2), "cores": nt,
+            "sample": f"{imgs} of the 32 images: dynamic quantise (amax over the batch), dequantise, direct conv "
+                      "(reference loop order kh, kw, channel) + bias + ReLU"}
 
 
 if __name__ == "__main__":

@@ -371,6 +371,16 @@ LCML_API int lcml_fp8_binary(int op, int dtype, const void *a, const int64_t *a_
                              const int64_t *b_shape, int b_ndim, void *y, const int64_t *y_shape, int y_ndim,
                              void *stream);
 
+/*
+ * Measurement aid, no counterpart in the reference: reads `bytes` bytes
+ * (a multiple of 16) at 16-byte aligned device pointer p with `workgroups`
+ * workgroups of 256 threads and does nothing else (`sink`: one device word,
+ * written only when a fold of the data equals a fixed constant).  Its time
+ * over a buffer is the HBM read floor that the bandwidth-bound small-M GEMM
+ * (which reads the same weight bytes once) is compared with.
+ */
+LCML_API int lcml_fp8_stream_read(const void *p, int64_t bytes, int workgroups, uint32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

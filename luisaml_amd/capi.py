@@ -70,6 +70,7 @@ _SIGS = {
     "lcml_fp8_sgemm": (_int, [_i64, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _f32, _vp, _int, _i64,
                               _i64, _f32, _int, _vp, _int, _i64, _vp]),
     "lcml_fp8_activation": (_int, [_vp, _vp, _i64, _int, _vp]),
+    "lcml_fp8_stream_read": (_int, [_vp, _i64, _int, _vp, _vp]),
 }
 
 
@@ -360,6 +361,14 @@ def activation(x: torch.Tensor, act: int, out: torch.Tensor | None = None, strea
     y = out if out is not None else torch.empty_like(x)
     _check(lib().lcml_fp8_activation(_ptr(x), _ptr(y), x.numel(), int(act), _stream(stream)))
     return y
+
+
+def stream_read(buf: torch.Tensor, sink: torch.Tensor, workgroups: int = 1024, stream=None) -> None:
+    """Read every byte of buf (contiguous, 16-byte multiple) and nothing else:
+    the HBM read floor for the same bytes.  sink: one int32/uint32 device word."""
+    assert buf.is_contiguous() and (buf.numel() * buf.element_size()) % 16 == 0
+    _check(lib().lcml_fp8_stream_read(_ptr(buf), buf.numel() * buf.element_size(), int(workgroups), _ptr(sink),
+                                      _stream(stream)))
 
 
 # ---------------------------------------------------- fp8 data-type ops ----

@@ -512,6 +512,16 @@ int lcml_fp8_activation(const float *x, float *y, int64_t n, int act, void *stre
     return hip_status(lcml::launch_activation(x, y, n, act, (hipStream_t)stream), "lcml_fp8_activation");
 }
 
+int lcml_fp8_stream_read(const void *p, int64_t bytes, int workgroups, uint32_t *sink, void *stream) {
+    const char *fn = "lcml_fp8_stream_read";
+    if (bytes < 0 || bytes % 16 != 0 || workgroups < 1 || workgroups > (1 << 20))
+        return fail(LCML_ERR_INVALID_ARG, "%s: bytes=%lld (multiple of 16) workgroups=%d", fn, (long long)bytes,
+                    workgroups);
+    if (bytes == 0) return LCML_OK;
+    if (!p || !sink || !aligned(p, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: p must be 16-byte aligned, sink set", fn);
+    return hip_status(lcml::launch_stream_read(p, bytes, workgroups, sink, (hipStream_t)stream), fn);
+}
+
 namespace {
 bool fp8_dtype_ok(int dt) {
     return dt == LCML_DTYPE_FLOAT || dt == LCML_DTYPE_FLOAT8E4M3FN || dt == LCML_DTYPE_FLOAT8E5M2;

@@ -284,6 +284,15 @@ __device__ inline void epi_store(const Epilogue &e, int64_t m, int64_t n, float 
         reinterpret_cast<float *>(e.y)[m * e.ldy + n] = v;
 }
 
+// columns n and n + 1 of row m in one store (n even, ldy even: the pair is
+// 4- or 8-byte aligned)
+__device__ inline void epi_store2(const Epilogue &e, int64_t m, int64_t n, float v0, float v1) {
+    if (e.y_bf16)
+        reinterpret_cast<uint32_t *>(e.y)[(m * e.ldy + n) >> 1] = (uint32_t)bf16_rne(v0) | ((uint32_t)bf16_rne(v1) << 16);
+    else
+        reinterpret_cast<float2 *>(e.y)[(m * e.ldy + n) >> 1] = float2{v0, v1};
+}
+
 // E4M3 -> bf16 (exact: every E4M3 value is a bf16 value; 0x7f/0xff -> NaN)
 // for 8 consecutive bytes (two dwords) with v_cvt_scalef32_pk_bf16_fp8 at
 // scale 1.0, giving one 8-element operand of the bf16 MFMAs.

@@ -94,6 +94,11 @@ struct BcastGeom {
 hipError_t launch_fp8_binary(int op, int fmt, const void *a, const void *b, void *y, int64_t n, bool same_shape,
                              const BcastGeom &g, hipStream_t s);
 
+// read-only stream over bytes (% 16 == 0) of 16-byte aligned p with
+// `workgroups` workgroups of 256 threads; sink: one word, written only when
+// the fold of the data equals a fixed constant
+hipError_t launch_stream_read(const void *p, int64_t bytes, int workgroups, uint32_t *sink, hipStream_t s);
+
 // A kernel's dynamic-LDS limit (hipFuncSetAttribute) is per device: set it
 // once per (kernel, device), tracked in `done` (bit d = device d; devices past
 // 63 set it on every call).  The call is idempotent, so two threads racing on
