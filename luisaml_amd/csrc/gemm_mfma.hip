@@ -162,6 +162,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         __builtin_amdgcn_make_buffer_rsrc((void *)(g.bp + (size_t)grp * g.b_bytes), 0, (int)g.b_bytes, 0x00020000);
     uint32_t a_off[T::A_BLK];
     int a_kc[T::A_BLK];
+    uint32_t a_klim[CONV ? 1 : T::A_BLK];  // K for rows in range, 0 for rows past M
     uint32_t b_off[T::B_BLK];
     int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
     // CONV: where the block's chunk of the next step to issue lies in (kh, kw, c)
@@ -192,6 +193,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             a_c[i] = cc; a_kw[i] = kw; a_kh[i] = kh;
         } else {
             a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
+            a_klim[i] = (m0 + r < g.M) ? (uint32_t)g.K : 0u;
         }
     }
 #pragma unroll
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                     if (++a_kw[i] == cv.KW) { a_kw[i] = 0; ++a_kh[i]; }
                 }
             } else {
-                off = (a_off[i] != OOB && (int64_t)kbyte + a_kc[i] < g.K) ? a_off[i] + kbyte : OOB;
+                off = kbyte + (uint32_t)a_kc[i] < a_klim[i] ? a_off[i] + kbyte : OOB;
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * T::A_BLK + i) * 1024), 16,
                                                      off, 0, 0, 0);
