@@ -35,19 +35,26 @@ namespace lcml::onnx {
 class PackedWeightTensor : public ITensor {
     DeviceArray<uint8_t> packed_;
     DeviceArray<float> scale_;
-    uint32_t K_, N_;
+    uint32_t K_, N_, batches_;
+    size_t batch_bytes_;
 
 public:
-    PackedWeightTensor(uint32_t K, uint32_t N, DeviceArray<uint8_t> packed, DeviceArray<float> scale)
-        : ITensor(shape_type{K, N}), packed_(std::move(packed)), scale_(std::move(scale)), K_(K), N_(N) {}
-    size_type size() const noexcept override { return K_ * N_; }
+    // `batches` packed [K, N] weights one after another (a MatMul weight
+    // [..., K, N]); the scale is per tensor or per output channel, shared by
+    // every batch
+    PackedWeightTensor(uint32_t K, uint32_t N, DeviceArray<uint8_t> packed, DeviceArray<float> scale,
+                       uint32_t batches = 1)
+        : ITensor(shape_type{K, N}), packed_(std::move(packed)), scale_(std::move(scale)), K_(K), N_(N),
+          batches_(batches), batch_bytes_(batches ? packed_.size() / batches : 0) {}
+    size_type size() const noexcept override { return batches_ * K_ * N_; }
     refl::TypeIndex element_type_index() const noexcept override { return refl::type_index_of<FP8E4M3FN>(); }
     std::string_view element_type_name() const noexcept override { return "FP8E4M3FN(packed)"; }
     bool is_constant() const noexcept override { return true; }
     void *device_data() const noexcept override { return packed_.data(); }
     uint32_t K() const { return K_; }
     uint32_t N() const { return N_; }
-    const uint8_t *packed() const { return packed_.data(); }
+    uint32_t batches() const { return batches_; }
+    const uint8_t *packed(size_t batch = 0) const { return packed_.data() + batch * batch_bytes_; }
     const float *scale() const { return scale_.data(); }
     bool per_channel() const { return scale_.size() > 1; }
 };

@@ -301,21 +301,39 @@ void NetworkInstance::fuse_qdq_linear() {
         const Variable &A = n.get_inputs()[0].get();
         const Variable &B = n.get_inputs()[1].get();
         // ---- B = DequantizeLinear(W_e4m3 constant, s_w [, 0]) ----
-        const Node *dqw = match_weight(B, i, 2);
+        // MatMul also takes a batched weight [..., K, N] (mat_mul.cpp:187-303):
+        // one packed weight per batch, batch dimensions right-aligned and
+        // broadcast against A's where they are 1
+        const size_t wrank = matmul && B.get_shape().size() >= 3 ? B.get_shape().size() : 2;
+        const Node *dqw = match_weight(B, i, wrank);
         if (!dqw) continue;
         const Variable &W = dqw->get_inputs()[0].get();
         const Variable &sw = dqw->get_inputs()[1].get();
         const bool w_is_nk = gemm && attr_int(n, "transB", 0) != 0;
-        const size_t N = w_is_nk ? W.get_shape()[0] : W.get_shape()[1];
-        const size_t K = w_is_nk ? W.get_shape()[1] : W.get_shape()[0];
+        const auto &wsh = W.get_shape();
+        const size_t N = w_is_nk ? wsh[0] : wsh[wrank - 1];
+        const size_t K = w_is_nk ? wsh[1] : wsh[wrank - 2];
         const size_t nscale = sw.num_elements();
         if (nscale != 1) {
             int axis = attr_int(*dqw, "axis", 1);
-            if (axis < 0) axis += 2;
-            const int n_axis = w_is_nk ? 0 : 1;
+            if (axis < 0) axis += (int)wrank;
+            const int n_axis = w_is_nk ? 0 : (int)wrank - 1;
             if (axis != n_axis || nscale != N) continue;  // only per-output-channel scales fuse
         }
         if (A.get_shape().empty()) continue;
+        std::vector<int32_t> wbatch;  // the weight's batch dimensions
+        if (wrank > 2) {
+            const auto &ash = A.get_shape();
+            if (ash.size() < 2) continue;  // a 1-D A against a batched weight stays unfused
+            const size_t ab = ash.size() - 2, bb = wrank - 2, nb = std::max(ab, bb);
+            bool bcast = true;
+            for (size_t d = 0; d < nb; ++d) {
+                const size_t ad = d + ab >= nb ? ash[d + ab - nb] : 1, bd = d + bb >= nb ? wsh[d + bb - nb] : 1;
+                bcast = bcast && (ad == bd || ad == 1 || bd == 1);
+            }
+            if (!bcast) continue;
+            for (size_t d = 0; d < bb; ++d) wbatch.push_back((int32_t)wsh[d]);
+        }
         if (trans_a ? (A.get_shape().size() != 2 || A.get_shape()[0] != K) : A.get_shape().back() != K) continue;
         // ---- A: static QDQ, dynamic QDQ, or fp32 ----
         ActQ aq = match_act(A, i);
@@ -337,7 +355,10 @@ void NetworkInstance::fuse_qdq_linear() {
         // nodes through different DequantizeLinear scales or transB packs twice
         std::string pname = W.get_name() + "::packed::" + sw.get_name() + (w_is_nk ? "::nk" : "::kn");
         if (!g.has_var(pname)) {
-            Variable pv(pname, DataType::FLOAT8E4M3FN, {K, N});
+            std::vector<size_t> pshape(wsh.begin(), wsh.end() - 2);  // batch dimensions, then [K, N]
+            pshape.push_back(K);
+            pshape.push_back(N);
+            Variable pv(pname, DataType::FLOAT8E4M3FN, pshape);
             pv.set_is_constant(true);
             g.add_variable(std::move(pv));
         }
@@ -357,6 +378,7 @@ void NetworkInstance::fuse_qdq_linear() {
         f.set_attribute(Attribute{"w_is_nk", (int32_t)w_is_nk});
         f.set_attribute(Attribute{"trans_a", (int32_t)trans_a});
         f.set_attribute(Attribute{"weight", W.get_name()});
+        if (!wbatch.empty()) f.set_attribute(Attribute{"wbatch", wbatch});
         for (size_t d : drop) removed[d] = true;
         replacement.emplace(i, std::move(f));
         ++fused_count_;
@@ -383,25 +405,32 @@ void NetworkInstance::pack_weights() {
         const Variable &sw = n.get_inputs()[2].get();
         create_tensor_for_var(W);
         create_tensor_for_var(sw);
-        const uint32_t K = (uint32_t)pv.get_shape()[0], N = (uint32_t)pv.get_shape()[1];
+        // [batch dimensions..., K, N]: one packed weight per batch
+        const auto &psh = pv.get_shape();
+        const uint32_t K = (uint32_t)psh[psh.size() - 2], N = (uint32_t)psh[psh.size() - 1];
+        uint32_t batches = 1;
+        for (size_t d = 0; d + 2 < psh.size(); ++d) batches *= (uint32_t)psh[d];
         const auto &ws = W.get_shape();
         const int64_t group = conv ? attr_int(n, "group", 1) : 1;
         // conv weights [cout, cin_g, kh, kw], or [cout, cin_g, kl] (1-D: kh = 1)
         const int64_t ckh = conv && ws.size() == 4 ? (int64_t)ws[2] : 1, ckw = conv ? (int64_t)ws.back() : 1;
+        const size_t batch_bytes = (size_t)lcml_fp8_packed_weight_bytes(K, N);
         DeviceArray<uint8_t> packed(conv ? (size_t)lcml_fp8_packed_conv_weight_bytes(ws[0], ws[1], ckh, ckw, group)
-                                         : (size_t)lcml_fp8_packed_weight_bytes(K, N));
+                                         : batch_bytes * batches);
         ITensor &wt = table_.at(W.get_name());
+        const uint8_t *wsrc = static_cast<const uint8_t *>(wt.device_data());
         if (conv)
-            lcml_check(lcml_fp8_pack_conv_weight(static_cast<const uint8_t *>(wt.device_data()), ws[0], ws[1], ckh, ckw,
-                                                 group, packed.data(), stream_),
+            lcml_check(lcml_fp8_pack_conv_weight(wsrc, ws[0], ws[1], ckh, ckw, group, packed.data(), stream_),
                        "pack conv weight");
         else
-            lcml_check(lcml_fp8_pack_weight(static_cast<const uint8_t *>(wt.device_data()), K, N,
-                                            attr_int(n, "w_is_nk", 0), packed.data(), stream_),
-                       "pack weight");
+            for (uint32_t b = 0; b < batches; ++b)
+                lcml_check(lcml_fp8_pack_weight(wsrc + (size_t)b * K * N, K, N, attr_int(n, "w_is_nk", 0),
+                                                packed.data() + b * batch_bytes, stream_),
+                           "pack weight");
         ITensor &st = table_.at(sw.get_name());
         DeviceArray<float> scale(static_cast<float *>(st.device_data()), 0, st.size());
-        table_.own(pv.get_name(), std::make_unique<PackedWeightTensor>(K, N, std::move(packed), std::move(scale)));
+        table_.own(pv.get_name(),
+                   std::make_unique<PackedWeightTensor>(K, N, std::move(packed), std::move(scale), batches));
     }
 }
 

@@ -136,16 +136,103 @@ public:
 // 2: A quantised with its dynamic per-tensor scale (amax/448).
 // trans_a: A is [K, M] (Gemm transA=1); the quantiser writes the [M, K]
 // E4M3 copy as a transposing NCHW -> NHWC quantise of a [1, K, 1, M] view.
+// wbatch: the batch dimensions of a batched MatMul weight [..., K, N] (empty
+// for a 2-D weight): one GEMM per output batch, A's and W's batch dimensions
+// right-aligned and broadcast where they are 1 (mat_mul.cpp:187-303); A is
+// quantised once, per tensor, as the unfused DynamicQuantizeLinear does.
 class FP8Linear : public StreamOperator {
     int a_mode_, has_c_, act_, trans_a_;
     float alpha_, beta_;
+    std::vector<int32_t> wbatch_;
     std::unique_ptr<DeviceBuffer> qa_, ws_, sx_;
     size_t qa_bytes_ = 0, ws_bytes_ = 0;
 
+    uint8_t *qa_scratch(size_t need) {
+        if (!qa_ || qa_bytes_ < need) {
+            qa_ = std::make_unique<DeviceBuffer>(need);
+            qa_bytes_ = need;
+        }
+        return static_cast<uint8_t *>(qa_->data());
+    }
+    void *dyn_workspace() {
+        if (!ws_ || ws_bytes_ < (size_t)LCML_FP8_DYNAMIC_WORKSPACE_BYTES) {
+            ws_ = std::make_unique<DeviceBuffer>((size_t)LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
+            ws_bytes_ = LCML_FP8_DYNAMIC_WORKSPACE_BYTES;
+        }
+        return ws_->data();
+    }
+    float *scale_slot() {
+        if (!sx_) sx_ = std::make_unique<DeviceBuffer>(sizeof(float));
+        return static_cast<float *>(sx_->data());
+    }
+
+    void forward_batched(ITensor &A, const PackedWeightTensor &W, ITensor *a_scale, ITensor &Y) {
+        const int an = (int)A.ndim();
+        const int64_t K = W.K(), N = W.N();
+        LCML_ASSERT(an >= 2 && (int64_t)A.shape(an - 1) == K, "FP8Linear: A must be [..., M, K=%lld]", (long long)K);
+        const int64_t M = A.shape(an - 2);
+        const int ab = an - 2, bb = (int)wbatch_.size(), nb = ab > bb ? ab : bb;
+        std::vector<int64_t> ydim(nb), astr(nb, 0), bstr(nb, 0);
+        int64_t sa = M * K, sb = 1;  // A in elements, W in packed batches
+        for (int d = nb - 1; d >= 0; --d) {
+            const int ai = d - (nb - ab), bi = d - (nb - bb);
+            const int64_t ad = ai >= 0 ? A.shape(ai) : 1, bd = bi >= 0 ? wbatch_[bi] : 1;
+            LCML_ASSERT(ad == bd || ad == 1 || bd == 1, "FP8Linear: batch dimensions %lld and %lld do not broadcast",
+                        (long long)ad, (long long)bd);
+            ydim[d] = ad > bd ? ad : bd;
+            if (ad > 1) astr[d] = sa;
+            if (bd > 1) bstr[d] = sb;
+            sa *= ad;
+            sb *= bd;
+        }
+        LCML_ASSERT(sb == (int64_t)W.batches(), "FP8Linear: %u packed weights for %lld weight batches", W.batches(),
+                    (long long)sb);
+        int64_t batches = 1;
+        for (int64_t v : ydim) batches *= v;
+        LCML_ASSERT((int64_t)Y.size() == batches * M * N, "FP8Linear: output has %u elements, expected %lld", Y.size(),
+                    (long long)(batches * M * N));
+        const int ydt = out_dtype_code(Y, "FP8Linear");
+        const size_t esz = ydt == LCML_DTYPE_BFLOAT16 ? 2 : 4;
+        const float *a = static_cast<const float *>(A.device_data());
+        char *y = static_cast<char *>(Y.device_data());
+        const uint8_t *q = nullptr;
+        const float *sa_dev = nullptr;
+        if (a_mode_ != 0) {  // the whole activation once: E4M3 codes and one per-tensor scale
+            uint8_t *qw = qa_scratch(A.size());
+            if (a_mode_ == 1) {
+                sa_dev = static_cast<const float *>(a_scale->device_data());
+                check(lcml_fp8_quantize(a, qw, 1, 1, A.size(), sa_dev, stream_), "FP8Linear quantize");
+            } else {
+                float *sx = scale_slot();
+                check(lcml_fp8_quantize_dynamic(a, qw, A.size(), sx, dyn_workspace(), stream_), "FP8Linear quantize");
+                sa_dev = sx;
+            }
+            q = qw;
+        }
+        std::vector<int64_t> idx(nb, 0);
+        for (int64_t t = 0; t < batches; ++t) {
+            int64_t ao = 0, bo = 0;
+            for (int d = 0; d < nb; ++d) {
+                ao += idx[d] * astr[d];
+                bo += idx[d] * bstr[d];
+            }
+            void *yt = y + (size_t)(t * M * N) * esz;
+            if (a_mode_ == 0)
+                check(lcml_fp8_gemm_w8a32(M, N, K, a + ao, K, W.packed(bo), W.scale(), W.per_channel(), alpha_, nullptr,
+                                          0, 0, 0, beta_, act_, yt, ydt, N, stream_),
+                      "FP8Linear");
+            else
+                check(lcml_fp8_gemm(M, N, K, q + ao, K, sa_dev, W.packed(bo), W.scale(), W.per_channel(), alpha_,
+                                    nullptr, 0, 0, 0, beta_, act_, yt, ydt, N, LCML_KERNEL_AUTO, stream_),
+                      "FP8Linear");
+            for (int d = nb - 1; d >= 0 && ++idx[d] == ydim[d]; --d) idx[d] = 0;
+        }
+    }
+
 public:
-    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta, int trans_a)
+    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta, int trans_a, std::vector<int32_t> wbatch)
         : StreamOperator("FP8Linear"), a_mode_(a_mode), has_c_(has_c), act_(act), trans_a_(trans_a), alpha_(alpha),
-          beta_(beta) {}
+          beta_(beta), wbatch_(std::move(wbatch)) {}
     void forward(std::span<std::reference_wrapper<ITensor>> inputs,
                  std::span<std::reference_wrapper<ITensor>> outputs) override {
         ITensor &A = inputs[0], &Y = outputs[0];
@@ -155,6 +242,11 @@ public:
         size_t next = 3;
         ITensor *a_scale = a_mode_ == 1 ? &inputs[next++].get() : nullptr;
         ITensor *C = has_c_ ? &inputs[next++].get() : nullptr;
+        if (!wbatch_.empty()) {
+            LCML_ASSERT(!C && !trans_a_, "FP8Linear: a batched weight takes no C and no transA");
+            forward_batched(A, *W, a_scale, Y);
+            return;
+        }
         const int64_t K = W->K(), N = W->N(), M = A.size() / K;
         LCML_ASSERT(M * K == (int64_t)A.size(), "FP8Linear: A has %u elements, not a multiple of K=%lld", A.size(),
                     (long long)K);
@@ -246,7 +338,8 @@ REGISTER_TO_DEFAULT_OPSET(Gelu) {
 REGISTER_TO_DEFAULT_OPSET(FP8Linear) {
     return std::make_unique<FP8Linear>(attr_int(node, "a_mode", 0), attr_int(node, "has_c", 0),
                                        attr_int(node, "act", 0), attr_float(node, "alpha", 1.0f),
-                                       attr_float(node, "beta", 1.0f), attr_int(node, "trans_a", 0));
+                                       attr_float(node, "beta", 1.0f), attr_int(node, "trans_a", 0),
+                                       attr_ints(node, "wbatch", {}));
 };
 
 }  // namespace lcml::onnx

@@ -841,6 +841,140 @@ static void test_memory_planner() {
 // fp32 MatMul with numpy semantics (mat_mul.cpp:187-303): 1-D operands and
 // right-aligned batch dimensions broadcast where they are 1; every output
 // batch against the oracle's GEMM of the matching A and B slices.
+// MatMul against a batched E4M3 weight [..., K, N] through DequantizeLinear
+// (per-tensor or per-output-channel scale on the last axis), with a dynamic
+// QDQ, a static QDQ or an fp32 activation: fused into one FP8Linear (one
+// packed weight per batch, batch dimensions broadcast as mat_mul.cpp:187-303)
+// and op by op, both against the oracle's per-batch Gemm of the dequantised
+// operands.
+static void test_batched_fp8_matmul(bool fused) {
+    std::printf("[18] MatMul with a batched E4M3 weight, dynamic / static / fp32 activation (%s)\n",
+                fused ? "fused" : "unfused");
+    struct Case {
+        std::vector<size_t> a, w, y;
+        bool per_channel;
+    };
+    const size_t M = 5, K = 64, N = 48;
+    const Case cases[] = {{{2, 3, M, K}, {3, K, N}, {2, 3, M, N}, true},
+                          {{M, K}, {2, K, N}, {2, M, N}, false},
+                          {{2, 1, M, K}, {1, 3, K, N}, {2, 3, M, N}, true}};
+    auto count = [](const std::vector<size_t> &v) {
+        size_t n = 1;
+        for (size_t d : v) n *= d;
+        return n;
+    };
+    int ci = 0;
+    for (const Case &c : cases) {
+        for (int mode = 0; mode < 3; ++mode) {  // 0: fp32 A, 1: static QDQ, 2: dynamic QDQ
+            const size_t na = count(c.a), nw = count(c.w), wb = nw / (K * N);
+            auto x = normals(300 + 10 * ci + mode, na, 1.0f), w = normals(400 + ci, nw, 0.05f);
+            std::vector<float> sw(c.per_channel ? N : 1, 0.0f);
+            for (size_t i = 0; i < nw; ++i) {
+                float &m = sw[c.per_channel ? i % N : 0];
+                m = std::max(m, std::fabs(w[i]));
+            }
+            for (auto &v : sw) v = orc_scale_from_amax(v);
+            std::vector<uint8_t> qw(nw), zp(1, 0);
+            if (c.per_channel)
+                orc_quantize(w.data(), qw.data(), nw / N, N, 1, sw.data());  // axis = last
+            else
+                orc_quantize(w.data(), qw.data(), 1, 1, nw, sw.data());
+            float sx = orc_scale_from_amax(orc_amax(x.data(), na));
+            Graph g("bmm");
+            Blob blob;
+            var(g, "x", DataType::FLOAT, c.a);
+            blob_var(g, blob, "W", DataType::FLOAT8E4M3FN, c.w, qw.data(), qw.size());
+            blob_var(g, blob, "sw", DataType::FLOAT, {sw.size()}, sw.data(), sw.size() * 4);
+            var(g, "Wf", DataType::FLOAT, c.w);
+            var(g, "y", DataType::FLOAT, c.y);
+            std::string a_in = "x";
+            if (mode == 1) {
+                raw_var(g, "sx", DataType::FLOAT, {1}, &sx, 4);
+                raw_var(g, "zx", DataType::FLOAT8E4M3FN, {1}, zp.data(), 1);
+                var(g, "xq", DataType::FLOAT8E4M3FN, c.a);
+                var(g, "xd", DataType::FLOAT, c.a);
+                node(g, "QuantizeLinear", {"x", "sx", "zx"}, {"xq"});
+                node(g, "DequantizeLinear", {"xq", "sx", "zx"}, {"xd"});
+                a_in = "xd";
+            } else if (mode == 2) {
+                var(g, "xq", DataType::FLOAT8E4M3FN, c.a);
+                var(g, "xs", DataType::FLOAT, {1});
+                var(g, "xz", DataType::FLOAT8E4M3FN, {1});
+                var(g, "xd", DataType::FLOAT, c.a);
+                node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
+                node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+                a_in = "xd";
+            }
+            if (c.per_channel)
+                node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"}, {Attribute{"axis", (int32_t)(c.w.size() - 1)}});
+            else
+                node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"});
+            node(g, "MatMul", {a_in, "Wf"}, {"y"});
+            g.add_input("x");
+            g.add_output("y");
+            Model m(10, "test", "1");
+            m.set_graph(std::move(g));
+            DeviceBuffer wbuf(blob.bytes.size());
+            CHECK(hipMemcpy(wbuf.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+            ITensor::shape_type as(c.a.begin(), c.a.end()), ys(c.y.begin(), c.y.end());
+            auto xt = upload(x, as);
+            auto yt = make_device_tensor<float>(ys);
+            NetworkInstance net;
+            net.set_model(std::move(m));
+            net.set_fusion(fused);
+            net.set_weight_buffer(wbuf.data(), blob.bytes.size());
+            net.set_input("x", *xt);
+            net.set_output("y", *yt);
+            net.forward();
+            auto y = download<float>(*yt);
+            if (fused)
+                CHECK(net.fused_linear_count() == 1 && net.executed_op_types() == std::vector<std::string>{"FP8Linear"});
+            else
+                CHECK(net.fused_linear_count() == 0);
+            // oracle: the activation as the graph sees it, the dequantised weight, one Gemm per output batch
+            std::vector<float> A(x), Bw(nw);
+            if (mode != 0) {
+                std::vector<uint8_t> qx(na);
+                orc_quantize(x.data(), qx.data(), 1, 1, na, &sx);
+                orc_dequantize(qx.data(), A.data(), 1, 1, na, &sx);
+            }
+            if (c.per_channel)
+                orc_dequantize(qw.data(), Bw.data(), nw / N, N, 1, sw.data());
+            else
+                orc_dequantize(qw.data(), Bw.data(), 1, 1, nw, sw.data());
+            std::vector<size_t> ab(c.a.begin(), c.a.end() - 2), bb(c.w.begin(), c.w.end() - 2);
+            const size_t nb = std::max(ab.size(), bb.size());
+            ab.insert(ab.begin(), nb - ab.size(), 1);
+            bb.insert(bb.begin(), nb - bb.size(), 1);
+            std::vector<size_t> yb(nb);
+            size_t batches = 1;
+            for (size_t d = 0; d < nb; ++d) batches *= (yb[d] = std::max(ab[d], bb[d]));
+            CHECK(y.size() == batches * M * N && wb >= 1);
+            std::vector<float> ref(y.size());
+            std::vector<double> bound(y.size());
+            for (size_t t = 0; t < batches; ++t) {
+                size_t rem = t, ai = 0, bi = 0, am = 1, bm = 1;
+                for (size_t d = nb; d-- > 0;) {
+                    const size_t coord = rem % yb[d];
+                    rem /= yb[d];
+                    ai += (ab[d] == 1 ? 0 : coord) * am;
+                    bi += (bb[d] == 1 ? 0 : coord) * bm;
+                    am *= ab[d];
+                    bm *= bb[d];
+                }
+                orc_gemm(M, N, K, A.data() + ai * M * K, 0, Bw.data() + bi * K * N, 0, 1.0f, 0.0f, nullptr, -1, 0, 0,
+                         0, ref.data() + t * M * N);
+                orc_gemm_abs_bound(M, N, K, A.data() + ai * M * K, 0, Bw.data() + bi * K * N, 0, 1.0f, 0.0f, nullptr,
+                                   -1, 0, 0, bound.data() + t * M * N);
+            }
+            char what[64];
+            std::snprintf(what, sizeof what, "batched fp8 matmul case %d mode %d", ci, mode);
+            CHECK(close(y, ref, bound, 1e-4, 0.0, what));
+        }
+        ++ci;
+    }
+}
+
 static void test_batched_matmul() {
     std::printf("[12] fp32 MatMul: batched, broadcast and 1-D operands\n");
     struct Case {
@@ -1326,6 +1460,8 @@ int main(int argc, char **argv) {
         test_qdq_conv(true, 2);
         test_f32_grouped_conv();
         test_batched_matmul();
+        test_batched_fp8_matmul(true);
+        test_batched_fp8_matmul(false);
         test_fp8_tensor_conv(false);
         test_fp8_tensor_conv(true);
         test_e5m2_qdq_cast();
