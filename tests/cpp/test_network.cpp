@@ -337,7 +337,10 @@ static void test_static_qdq_gelu(int K = 256) {
     orc_gemm(M, N, K, A.data(), 0, Bw.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, 2, ref.data());
     std::vector<double> bound((size_t)M * N);
     orc_gemm_abs_bound(M, N, K, A.data(), 0, Bw.data(), 1, 1.0f, 1.0f, b.data(), 1, N, 0, bound.data());
-    CHECK(close(z, ref, bound, 1.13e-4, 1e-6, "static qdq gelu"));
+    // GELU: 1.13 x the summation-order bar plus twice the device's pinned
+    // evaluation difference (8 * 2^-24 of the pre-activation, which the
+    // bound dominates; tests/test_gpu_activation.py)
+    CHECK(close(z, ref, bound, 1.13e-4 + 16.0 * 0x1p-24, 0.0, "static qdq gelu"));
 }
 
 static void test_dynamic_qdq_matmul(int K = 512) {
@@ -1322,7 +1325,7 @@ static void test_tied_weight_two_layouts() {
     for (size_t i = 0; i < h.size(); ++i) ah[i] = std::fabs(h[i]) + (float)bound_h[i];
     for (size_t i = 0; i < W2.size(); ++i) aw[i] = std::fabs(W2[i]);
     orc_gemm_abs_bound(M, D, D, ah.data(), 0, aw.data(), 0, 1.0f, 0.0f, nullptr, -1, 0, 0, bound.data());
-    CHECK(close(y, ref, bound, 1e-4, 1e-6, "tied weight"));
+    CHECK(close(y, ref, bound, 1e-4, 0.0, "tied weight"));
 }
 
 // Gemm(transA=1): A is [K, M]; with a static or dynamic activation QDQ it

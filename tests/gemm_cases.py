@@ -18,6 +18,25 @@ from luisaml_amd import capi, synth
 
 TOL_ELEM = 1e-4
 TOL_FROB = 1e-5
+# The device GELU's evaluation differs from the oracle's fp32 evaluation of
+# the same formula by at most GELU_EVAL_C * 2^-24 * |x| (measured 6.2 for the
+# erf form, 3.4 for tanh; pinned by tests/test_gpu_activation.py).
+GELU_EVAL_C = 8.0
+
+
+def gelu_tol(act) -> float:
+    """Elementwise tolerance factor on the bound sum|a*b| + |beta*C| of an output.
+
+    Without an activation (or with ReLU, 1-Lipschitz and exact) it is the
+    summation-order bar TOL_ELEM.  GELU is 1.13-Lipschitz, so a pre-activation
+    error of TOL_ELEM * bound becomes at most 1.13 times that; the device's
+    evaluation of GELU adds GELU_EVAL_C * 2^-24 * |pre-activation| <=
+    GELU_EVAL_C * 2^-24 * bound, and the oracle's own fp32 evaluation at the
+    slightly different pre-activation as much again.
+    """
+    if act in (oracle.ACT_NONE, oracle.ACT_RELU):
+        return TOL_ELEM
+    return 1.13 * TOL_ELEM + 2.0 * GELU_EVAL_C * 2.0 ** -24
 
 
 class Case:
@@ -61,9 +80,7 @@ def reference(c, bias=None, alpha=1.0, beta=1.0, act=oracle.ACT_NONE):
 def assert_close(y, ref, bound, act=oracle.ACT_NONE, frob=True):
     y = np.asarray(y, np.float64)
     ref = np.asarray(ref, np.float64)
-    # GELU is 1.13-Lipschitz; its device evaluation adds a few ulp of |y|.
-    lip = 1.0 if act in (oracle.ACT_NONE, oracle.ACT_RELU) else 1.13
-    tol = TOL_ELEM * lip * bound + (0.0 if act in (oracle.ACT_NONE, oracle.ACT_RELU) else 1e-6 * np.abs(ref))
+    tol = gelu_tol(act) * bound
     d = np.abs(y - ref)
     bad = np.argwhere(~(d <= tol))
     assert bad.size == 0, (f"{len(bad)} elements outside tolerance; first {bad[:4].tolist()}: "
