@@ -133,6 +133,27 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 __device__ inline int a_swz(int r) { return (r / (256 / BK)) & (CPR - 1); }
 __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) << 4); }
 
+// Scheduling pattern for one step of the native FP8 loop: the NL
+// global->LDS loads first (the LDS reads may not pass them: the compiler
+// cannot tell the loads' LDS writes from the reads' addresses), then NM
+// MFMAs, each followed by its share of the next step's NR LDS fragment reads,
+// the reads spread over all but the last TAIL MFMAs, which cover the latency
+// of the final reads before the next barrier's wait.  Against the same loop
+// with the reads issued as one burst (the LDS command FIFO filled, stalling
+// the in-order issue of the MFMAs behind them): +3-4% at 8192^3 and on the
+// M=4096 linears, bit-identical.
+template <int NM, int NR, int NL, int TAIL = 4, int R = 0>
+__device__ __forceinline__ void sched_interleave() {
+    if constexpr (R == 0) __builtin_amdgcn_sched_group_barrier(0x020, NL, 0);  // global->LDS loads
+    if constexpr (R < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        constexpr int NMR = NM > TAIL ? NM - TAIL : NM;  // MFMAs that take reads
+        constexpr int rd = R < NMR ? (NR * (R + 1)) / NMR - (NR * R) / NMR : 0;
+        if constexpr (rd > 0) __builtin_amdgcn_sched_group_barrier(0x100, rd, 0);  // LDS reads
+        sched_interleave<NM, NR, NL, TAIL, R + 1>();
+    }
+}
+
 template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV, bool PP>
 __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_gemm_mfma(GemmArgs g) {
     using T = Tile<WAVES_M, WAVES_N, WM, WN>;
@@ -268,6 +289,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     // written out because the compiler's own accounting would wait for every
     // load; sched_barrier(0) keeps LDS reads and MFMAs on their side of it.
     auto step_sync = [&](auto outstanding) {
+        if constexpr (!EXACT) __builtin_amdgcn_sched_barrier(0);  // the step's MFMAs stay above the barrier
         __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(decltype(outstanding)::value) : "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -432,18 +454,21 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                                                                                 join(fb[j][0], fb[j][1]), acc[i][j], 0,
                                                                                 0, 0, 0, 0, 0);
         };
+        // the step's MFMAs and the next step's fragment reads are issued
+        // interleaved (sched_interleave), not as a burst of reads first
+        auto interleave = [&]() { sched_interleave<WM * WN, 2 * (WM + WN), T::LOADS>(); };
         read_frag(a0, b0, 0);
         for (int kt = 0; kt < g.nk; kt += 2) {
             step_sync(Steady{});  // tile kt+1
             issue_tile(kt + NSTAGE - 1, (kt + NSTAGE - 1) % NSTAGE);
             read_frag(a1, b1, kt + 1);
-            __builtin_amdgcn_sched_barrier(0);
             mma(a0, b0);
+            interleave();
             step_sync(Steady{});  // tile kt+2
             issue_tile(kt + NSTAGE, (kt + NSTAGE) % NSTAGE);
             read_frag(a0, b0, kt + 2);  // past the end: an unused stage
-            __builtin_amdgcn_sched_barrier(0);
             mma(a1, b1);
+            interleave();
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tail's loads land before the LDS is reused
