@@ -146,6 +146,25 @@ def test_conv_bf16_out_and_per_tensor_weight_scale(dev):
     assert np.array_equal(y16.view(torch.int16).cpu().numpy().view(np.uint16), oracle.bf16_rne(y32.cpu().numpy()))
 
 
+@pytest.mark.parametrize("act", [capi.ACT_GELU_ERF, capi.ACT_GELU_TANH])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_conv_gelu_epilogue(dev, act, with_bias):
+    """The NCHW epilogue specialised per activation, bias and output type:
+    GELU with and without bias against the oracle, bf16 = bf16_rne of fp32."""
+    n, c, h, w, cout, k = 2, 32, 11, 9, 40, 3
+    x, qw, ws = conv_case(n, c, h, w, cout, k, k, seed=act * 5 + with_bias, dev=dev)
+    bias = synth.normal(79, (cout,), std=0.01) if with_bias else None
+    xq, sx = capi.quantize_nhwc(to_dev(x, dev))
+    bp = capi.pack_conv_weight(to_dev(qw, dev))
+    d_bias = None if bias is None else to_dev(bias, dev)
+    y32 = capi.conv2d(xq, sx, bp, to_dev(ws, dev), cout, (k, k), pads=(1, 1), bias=d_bias, act=act)
+    y16 = capi.conv2d(xq, sx, bp, to_dev(ws, dev), cout, (k, k), pads=(1, 1), bias=d_bias, act=act,
+                      out_dtype=torch.bfloat16)
+    ref, bound = reference(x, qw, ws, bias, 1, 1, 1, act)
+    assert_close(y32.cpu().numpy(), ref, bound, act=act)
+    assert np.array_equal(y16.view(torch.int16).cpu().numpy().view(np.uint16), oracle.bf16_rne(y32.cpu().numpy()))
+
+
 def test_conv_native_fp8_close(dev):
     n, c, h, w, cout, k = 1, 64, 14, 14, 64, 3
     x, qw, ws = conv_case(n, c, h, w, cout, k, k, seed=9, dev=dev)

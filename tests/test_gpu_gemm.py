@@ -133,6 +133,70 @@ def test_bf16_output_is_rne_of_fp32(dev, kernel, act):
     assert np.array_equal(got, oracle.bf16_rne(y32))
 
 
+OUT_LAYOUTS = ["dense", "pitch_even", "pitch_odd", "misaligned", "rows_past_m"]
+
+
+def out_view(layout, M, N, dtype, dev, fill):
+    """An output [M, N] view in a larger buffer filled with `fill`: a padded
+    even or odd row pitch, a start one element past an aligned address, or
+    64 rows of buffer beyond row M."""
+    if layout == "dense":
+        buf = torch.full((M, N), fill, dtype=dtype, device=dev)
+        return buf, buf
+    if layout in ("pitch_even", "pitch_odd"):
+        ld = N + (16 if layout == "pitch_even" else 17)
+        buf = torch.full((M, ld), fill, dtype=dtype, device=dev)
+        return buf, buf[:, :N]
+    if layout == "misaligned":
+        buf = torch.full((M * N + 1,), fill, dtype=dtype, device=dev)
+        return buf, buf[1:].view(M, N)
+    buf = torch.full((M + 64, N), fill, dtype=dtype, device=dev)
+    return buf, buf[:M]
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "mfma_128", "mfma_fp8"])
+@pytest.mark.parametrize("layout", OUT_LAYOUTS)
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [320, 257])
+def test_mfma_epilogue_layouts(dev, kernel, layout, out_dtype, N):
+    """The tile kernels' row-major epilogue has a path specialised for the
+    activation, C and output type (taken when N and the row pitch are even,
+    the output is aligned and C does not vary over rows) and a general one;
+    both give the same bits, write nothing outside the [M, N] view, and
+    match the oracle.  The reference is the same kernel into a dense fp32
+    output (bf16: its bf16_rne)."""
+    M = 300
+    c = make_case(M, N, 512, seed=N + 11, dev=dev)
+    bias = make_bias("N", M, N, seed=5)
+    kw = dict(bias=bias, alpha=0.75, act=capi.ACT_GELU_TANH)
+    y32 = run(c, KERNELS[kernel], dev=dev, **kw).cpu().numpy()
+    if kernel != "mfma_fp8":
+        ref, bound = reference(c, bias=bias, alpha=0.75, act=capi.ACT_GELU_TANH)
+        assert_close(y32, ref, bound, act=capi.ACT_GELU_TANH)
+    fill = -12345.0
+    buf, view = out_view(layout, M, N, out_dtype, dev, fill)
+    d_bias = torch.from_numpy(bias).to(dev)
+    capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, c=d_bias, alpha=0.75, act=capi.ACT_GELU_TANH,
+              out=view, kernel=KERNELS[kernel])
+    torch.cuda.synchronize()
+    got = view.cpu()
+    if out_dtype == torch.bfloat16:
+        assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), oracle.bf16_rne(y32))
+    else:
+        assert np.array_equal(got.numpy().view(np.uint32), y32.view(np.uint32))
+    # everything outside the view keeps the fill value
+    mask = torch.ones_like(buf, dtype=torch.bool)
+    if layout == "misaligned":
+        mask[1:] = False
+    elif layout in ("pitch_even", "pitch_odd"):
+        mask[:, :N] = False
+    elif layout == "rows_past_m":
+        mask[:M] = False
+    else:
+        mask[:] = False
+    assert bool((buf.cpu()[mask.cpu()] == fill).all())
+
+
 def test_kernels_agree_small_m(dev):
     """All three kernels on one decode-shaped case agree within the bound."""
     c = make_case(16, 2048, 4096, seed=21, dev=dev)
