@@ -62,7 +62,7 @@ constexpr int BK = 64;                    // K per pipeline step
 constexpr int NSTAGE = LCML_GEMM_STAGES;  // LDS ring depth: NSTAGE-1 steps of loads in flight
 constexpr int CPR = BK / 16;              // 16-byte chunks per A row per step
 constexpr int GROUP_M = 8;
-constexpr int EP_PITCH = 33;   // CONV epilogue staging row pitch (floats)
+constexpr int EP_PITCH = 36;   // CONV epilogue staging row pitch (floats): 16-byte rows with 4 floats of padding, b128 reads conflict-free
 constexpr int EP2_PITCH = 72;  // row-major epilogue staging row pitch (floats)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -70,6 +70,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 // Tile geometry: WAVES_M x WAVES_N wavefronts, each owning WM x WN blocks of
@@ -184,21 +185,20 @@ __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, in
     }
 }
 
-// The NCHW epilogue's column loop with the same compile-time choices: lane l
-// writes its output pixel of columns colb .. colb + ncol - 1 (address p for
-// column colb, `step` elements per column), the column's scale and beta * C
-// taken from lane c of sc_l and cb_l.
+// The NCHW epilogue's column loop with the same compile-time choices (ACT < 0:
+// the activation taken from e.act at run time): lane l writes its output
+// pixel of columns colb .. colb + ncol - 1 (address p for column colb,
+// `step` elements per column), the column's scale and beta * C taken from
+// lane c of sc_l and cb_l.
 template <int ACT, bool HAS_C, bool BF16>
 __device__ __forceinline__ void epi_cols(const Epilogue &e, const float *srow, void *p, int64_t step, int ncol,
                                          int sc_l, int cb_l) {
 #pragma clang fp contract(off)  // as in epi_rows
     const float alpha = e.alpha;
-    // a rolled loop: v_readlane is convergent, so the compiler does not
-    // unroll around it; the stores do not wait, so several are in flight
-    for (int c = 0; c < ncol; ++c) {
-        float v = srow[c] * __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc_l, c)) * alpha;
+    auto put = [&](int c, float acc) {
+        float v = acc * __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc_l, c)) * alpha;
         if constexpr (HAS_C) v += __builtin_bit_cast(float, __builtin_amdgcn_readlane(cb_l, c));
-        v = apply_act(v, ACT);
+        v = apply_act(v, ACT < 0 ? e.act : ACT);
         if constexpr (BF16) {
             const f2 vv = {v, 0.0f};
             reinterpret_cast<uint16_t *>(p)[c * step] =
@@ -206,6 +206,28 @@ __device__ __forceinline__ void epi_cols(const Epilogue &e, const float *srow, v
         } else {
             reinterpret_cast<float *>(p)[c * step] = v;
         }
+    };
+    if (ncol == 32) {
+        // a whole block: four staged columns per 16-byte read, the next read
+        // issued before the current four are stored (the read past the last
+        // group lands in the row's padding), so an LDS round trip is paid
+        // once per four columns and overlapped.  Rolled: unrolling all 32
+        // columns of every specialisation doubled the kernel's code and made
+        // the whole conv 40% slower.
+        f4 a = *reinterpret_cast<const f4 *>(srow);
+#pragma unroll 1
+        for (int q = 0; q < 8; ++q) {
+            const f4 next = *reinterpret_cast<const f4 *>(srow + 4 * q + 4);
+            put(4 * q, a.x);
+            put(4 * q + 1, a.y);
+            put(4 * q + 2, a.z);
+            put(4 * q + 3, a.w);
+            a = next;
+        }
+    } else {
+        // a rolled loop: v_readlane is convergent, so the compiler does not
+        // unroll around it; the stores do not wait, so several are in flight
+        for (int c = 0; c < ncol; ++c) put(c, srow[c]);
     }
 }
 
@@ -590,7 +612,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             // lanes that the row test may have switched off
             asm volatile("" : "+v"(sc_l), "+v"(cb_l));
 
-#pragma unroll
+#pragma unroll 1
             for (int h = 0; h < WM / 2; ++h) {
                 const int rl = h * 64 + lane;
                 const int64_t m = m0 + wm * WM * 32 + rl;
@@ -617,12 +639,16 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                             else
                                 by_out(act, std::false_type{});
                         };
-                        switch (e.act) {
-                        case ACT_RELU: by_c(std::integral_constant<int, ACT_RELU>{}); break;
-                        case ACT_GELU_ERF: by_c(std::integral_constant<int, ACT_GELU_ERF>{}); break;
-                        case ACT_GELU_TANH: by_c(std::integral_constant<int, ACT_GELU_TANH>{}); break;
-                        default: by_c(std::integral_constant<int, ACT_NONE>{}); break;
-                        }
+                        // the conv's usual activations specialised; the GELU
+                        // forms share one instance that reads e.act (fewer
+                        // copies of the loop: the kernel's code size costs
+                        // time in every phase)
+                        if (e.act == ACT_RELU)
+                            by_c(std::integral_constant<int, ACT_RELU>{});
+                        else if (e.act == ACT_NONE)
+                            by_c(std::integral_constant<int, ACT_NONE>{});
+                        else
+                            by_c(std::integral_constant<int, -1>{});
                     } else {
 #pragma unroll 1
                         for (int c = 0; c < ncol; ++c) {
