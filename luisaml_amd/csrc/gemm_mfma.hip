@@ -74,9 +74,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 // Tile geometry: WAVES_M x WAVES_N wavefronts, each owning WM x WN blocks of
-// 32x32 outputs: 256x256 tiles of 2x4 wavefronts of 128x64 (both MFMA
-// kinds) or of 2x2 wavefronts of 128x128 (native FP8, one wavefront per
-// SIMD, a five-stage ring), and 128x128 tiles of 2x2 wavefronts of 64x64.
+// 32x32 outputs: 256x256 tiles of 2x4 wavefronts of 128x64 or of 2x2
+// wavefronts of 128x128 (one wavefront per SIMD, a five-stage ring), and
+// 128x128 tiles of 2x2 wavefronts of 64x64.
 template <int WAVES_M, int WAVES_N, int WM, int WN>
 struct Tile {
     static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
@@ -503,23 +503,26 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             asm volatile("s_barrier" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
-    } else if constexpr (!EXACT && !CONV && T::ONE_PER_SIMD) {
-        // Native FP8 with one wavefront per SIMD (2x2 wavefronts of 128x128):
-        // a step reads 64 KB of fragments from the LDS instead of the 2x4
-        // layout's 96 KB.  Nothing shares a SIMD with the wavefront, so each
-        // step's instructions are placed explicitly: 2 MFMAs, the barrier,
-        // then 14 MFMAs with the next step's 16 fragment reads two per MFMA
-        // on the first 8 of them and this wavefront's 8 loads of step
-        // kt+NSTAGE-1 on the last 6 (their stage was last read two steps
-        // ago).  A 5-stage ring keeps 2.5 steps of loads in flight.  Load
-        // offsets and the LDS destination (M0) are plain adds, the k-range
-        // test only in the steps whose loads reach past K.  Against the 2x4
-        // schedule on MI355X: 8192^3 +5-7%, the M = 4096 O- and
-        // down-projections +3-4%, QKV +1% (bit-identical results); it loses
-        // 3% with an fp32 output (up-projection + GELU) and 6% on grids of
-        // one tile column, which keep the 2x4 layout.
+    } else if constexpr (!CONV && T::ONE_PER_SIMD) {
+        // One wavefront per SIMD (2x2 wavefronts of 128x128): a step reads
+        // 64 KB of fragments from the LDS instead of the 2x4 layout's 96 KB,
+        // and the exact instantiation widens 128 instead of 192 fragment
+        // values per lane and SIMD.  Nothing shares a SIMD with the
+        // wavefront, so each step's instructions are placed explicitly
+        // (sched_barrier between groups): 2 MFMAs, the barrier, then the
+        // next step's 16 fragment reads and this wavefront's 8 loads of step
+        // kt+NSTAGE-1 (whose stage was last read two steps ago) spread
+        // between the MFMAs.  A 5-stage ring keeps 2.5 steps of loads in
+        // flight.  Load offsets and the LDS destination (M0) are plain adds,
+        // the k-range test only in the steps whose loads reach past K.
+        // Against the 2x4 layout on MI355X (bit-identical results): 8192^3
+        // +5-7% native FP8, +3% exact; the M = 4096 O- and down-projections
+        // +3-4% FP8, +2-3% exact; QKV +1%.  With an fp32 output (the 128x128
+        // wavefront tiles' epilogue on 4 wavefronts costs more than the loop
+        // gains) and on grids of one tile column it loses 3-6%; those keep
+        // the 2x4 layout.
         constexpr int NF = WM + WN;
-        u4 f0[NF][2], f1[NF][2];
+        u4 f0[NF][2], f1[NF][2];  // raw E4M3 fragments [A0..A3, B0..B3][16-byte chunk]
         // per-lane offsets within a stage of the 16 chunk reads, in the order
         // the first MFMAs of a step use them: A0, B0..B3, A1..A3
         int roff[16];
@@ -535,51 +538,112 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             return f[blk == 0 ? 0 : blk <= 4 ? WM + blk - 1 : blk - 4][q & 1];
         };
         const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-        // rso: stage offset of step kt+1 (read), lso: of step kt+NSTAGE-1 (loaded)
-        auto step = [&](u4 (&fc)[NF][2], u4 (&fn)[NF][2], int kt, int rso, int lso, bool checked) {
-            auto mma = [&](int b) {
-                const int i = b / WN, j = b % WN;
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                    join(fc[i][0], fc[i][1]), join(fc[WM + j][0], fc[WM + j][1]), acc[i][j], 0, 0, 0, 0, 0, 0);
-            };
-            const uint8_t *rst = stage0 + rso;
-            uint8_t *lst = smem + lso;
-            const int lt = kt + NSTAGE - 1;
+        auto read = [&](u4 (&f)[NF][2], const uint8_t *st, int q) {
+            frag(f, q) = *reinterpret_cast<const u4 *>(st + roff[q]);
+        };
+        // load l (A blocks, then B) of step lt into the stage at `lst`
+        auto load = [&](uint8_t *lst, int lt, int l, bool checked) {
             const uint32_t kbyte = (uint32_t)lt * BK;
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fc landed
-            mma(0);
-            mma(1);
+            if (l < T::A_BLK) {
+                uint32_t off = a_off[l] + kbyte;  // rows past M: OOB + kbyte, still out of range
+                if (checked) off = kbyte + (uint32_t)a_kc[l] < a_klim[l] ? off : OOB;
+                lds_load16(a_rsrc, lst + (wave_u * T::A_BLK + l) * 1024, off);
+            } else {
+                lds_load16(b_rsrc, lst + T::A_BYTES + (wave_u * T::B_BLK + l - T::A_BLK) * 1024,
+                           b_off[l - T::A_BLK] + (uint32_t)lt * CPR * 1024);
+            }
+        };
+        auto sync_step = [&]() {
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(Steady::value) : "memory");
             __builtin_amdgcn_sched_barrier(0);
-            int l = 0;
+        };
+        // exact: the widened 16-k substeps, converted one substep ahead
+        bf16x8 cv0[EXACT ? NF : 1], cv1[EXACT ? NF : 1];
+        auto conv = [&](bf16x8 (&o)[EXACT ? NF : 1], const u4 (&f)[NF][2], int sub, int x) {
+            const u4 &w = f[x][sub >> 1];
+            o[x] = (sub & 1) ? e4m3x8_to_bf16(w.z, w.w) : e4m3x8_to_bf16(w.x, w.y);
+        };
+        // rso: stage offset of step kt+1 (read), lso: of step kt+NSTAGE-1 (loaded)
+        auto step = [&](u4 (&fc)[NF][2], u4 (&fn)[NF][2], int kt, int rso, int lso, bool checked) {
+            const uint8_t *rst = stage0 + rso;
+            uint8_t *lst = smem + lso;
+            const int lt = kt + NSTAGE - 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (EXACT) {
+                // 4 substeps of 16 bf16 MFMAs; each substep widens the next
+                // one's fragments (two conversions per MFMA), the last one
+                // the next step's first substep
+                auto mma = [&](const bf16x8 (&o)[NF], int b) {
+                    const int i = b / WN, j = b % WN;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o[i], o[WM + j], acc[i][j], 0, 0, 0);
+                };
+                // substep 0: the barrier after 2 MFMAs, then 14 reads
 #pragma unroll
-            for (int b = 2; b < 16; ++b) {
-                mma(b);
-                if (b < 10) {
-#pragma unroll
-                    for (int q = 2 * (b - 2); q < 2 * (b - 1); ++q)
-                        frag(fn, q) = *reinterpret_cast<const u4 *>(rst + roff[q]);
-                } else {
-                    // 8 loads over the last 6 MFMAs
-#pragma unroll
-                    for (int n = (T::LOADS - l + 15 - b) / (16 - b); n > 0; --n, ++l) {
-                        if (l < T::A_BLK) {
-                            uint32_t off = a_off[l] + kbyte;  // rows past M: OOB + kbyte, still out of range
-                            if (checked) off = kbyte + (uint32_t)a_kc[l] < a_klim[l] ? off : OOB;
-                            lds_load16(a_rsrc, lst + (wave_u * T::A_BLK + l) * 1024, off);
-                        } else {
-                            lds_load16(b_rsrc, lst + T::A_BYTES + (wave_u * T::B_BLK + l - T::A_BLK) * 1024,
-                                       b_off[l - T::A_BLK] + (uint32_t)lt * CPR * 1024);
-                        }
-                    }
+                for (int b = 0; b < 16; ++b) {
+                    mma(cv0, b);
+                    if ((b & 1) == 0) conv(cv1, fc, 1, b >> 1);
+                    if (b >= 2) read(fn, rst, b - 2);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (b == 1) sync_step();
                 }
+                // substep 1: the last 2 reads, the 8 loads
+#pragma unroll
+                for (int b = 0; b < 16; ++b) {
+                    mma(cv1, b);
+                    if ((b & 1) == 0) conv(cv0, fc, 2, b >> 1);
+                    if (b < 2) read(fn, rst, 14 + b);
+                    if (b >= 2 && b < 2 + T::LOADS) load(lst, lt, b - 2, checked);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int b = 0; b < 16; ++b) {
+                    mma(cv0, b);
+                    if ((b & 1) == 0) conv(cv1, fc, 3, b >> 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fn landed
                 __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int b = 0; b < 16; ++b) {
+                    mma(cv1, b);
+                    if ((b & 1) == 0) conv(cv0, fn, 0, b >> 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                // 16 FP8 MFMAs: reads two per MFMA on the 8 after the
+                // barrier, the 8 loads on the last 6
+                auto mma = [&](int b) {
+                    const int i = b / WN, j = b % WN;
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        join(fc[i][0], fc[i][1]), join(fc[WM + j][0], fc[WM + j][1]), acc[i][j], 0, 0, 0, 0, 0, 0);
+                };
+                __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fc landed
+                mma(0);
+                mma(1);
+                sync_step();
+                int l = 0;
+#pragma unroll
+                for (int b = 2; b < 16; ++b) {
+                    mma(b);
+                    if (b < 10) {
+                        read(fn, rst, 2 * (b - 2));
+                        read(fn, rst, 2 * (b - 2) + 1);
+                    } else {
+#pragma unroll
+                        for (int n = (T::LOADS - l + 15 - b) / (16 - b); n > 0; --n, ++l) load(lst, lt, l, checked);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         };
 #pragma unroll
-        for (int q = 0; q < 16; ++q) frag(f0, q) = *reinterpret_cast<const u4 *>(stage_a(0) + roff[q]);
+        for (int q = 0; q < 16; ++q) read(f0, stage_a(0), q);
+        if constexpr (EXACT) {
+            __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+#pragma unroll
+            for (int x = 0; x < NF; ++x) conv(cv0, f0, 0, x);
+        }
         int rso = T::STAGE, lso = (NSTAGE - 1) * T::STAGE;
         auto adv = [&]() {
             rso = rso + T::STAGE == NSTAGE * T::STAGE ? 0 : rso + T::STAGE;
@@ -901,9 +965,8 @@ using Shipped = Tile<WAVES_M, WAVES_N, WM, WN>;
 // CUs idle.
 using Small = Tile<2, 2, 2, 2>;
 
-// 256x256 tiles of 2x2 wavefronts of 128x128, native FP8 only: one
-// wavefront per SIMD and a five-stage ring (the k_gemm_mfma loop for
-// Tile::ONE_PER_SIMD).
+// 256x256 tiles of 2x2 wavefronts of 128x128: one wavefront per SIMD and
+// a five-stage ring (the k_gemm_mfma loop for Tile::ONE_PER_SIMD).
 using Wide = Tile<2, 2, 4, 4>;
 
 template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false>
@@ -940,14 +1003,14 @@ static_assert(!LCML_GEMM_PINGPONG || (WAVES_M == 2 && WAVES_M * WAVES_N == 8), "
 // at 8192^3 and the M = 4096 transformer and conv shapes it is 1-4% faster
 // (bitwise-identical results); the native-FP8 one keeps the interleaved
 // schedule (mixed: -8% on the conv, within +-1% elsewhere).
-// The native-FP8 GEMM takes the one-wavefront-per-SIMD layout where it
-// measured faster: a bf16 output (with fp32 the epilogue of its 128x128
-// wavefront tiles costs more than the main loop gains) on a grid of more
-// than one tile column.
+// The GEMM takes the one-wavefront-per-SIMD layout where it measured
+// faster: a bf16 output (with fp32 the epilogue of its 128x128 wavefront
+// tiles costs more than the main loop gains) on a grid of more than one
+// tile column.
 template <bool EXACT, bool CONV>
 hipError_t launch(GemmArgs &g, hipStream_t s) {
-    if constexpr (!EXACT && !CONV)
-        if (g.e.y_bf16 && g.N > Wide::BN) return launch_cfg<Wide, 2, 2, 4, 4, false, false>(g, s);
+    if constexpr (!CONV)
+        if (g.e.y_bf16 && g.N > Wide::BN) return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false>(g, s);
     return launch_cfg<Shipped, WAVES_M, WAVES_N, WM, WN, EXACT, CONV, EXACT && (bool)LCML_GEMM_PINGPONG>(g, s);
 }
 
