@@ -523,23 +523,26 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // the 2x4 layout.
         constexpr int NF = WM + WN;
         u4 f0[NF][2], f1[NF][2];  // raw E4M3 fragments [A0..A3, B0..B3][16-byte chunk]
-        // per-lane offsets within a stage of the 16 chunk reads, in the order
-        // the first MFMAs of a step use them: A0, B0..B3, A1..A3
-        int roff[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int blk = q >> 1, c = kgrp + (q & 1);
-            roff[q] = blk == 0 ? a_lds_off(a_r0, c)
-                    : blk <= 4 ? T::A_BYTES + b_off_lds[blk - 1] + c * 1024
-                               : a_lds_off(a_r0 + (blk - 4) * 32, c);
-        }
+        // The 16 chunk reads of a step, q = 0..15 in the order the first
+        // MFMAs of a step use them: A0, B0..B3, A1..A3 (two chunks each).
+        // Three per-lane bases and compile-time offsets address them: the A
+        // row blocks a_r0 + 32i share one swizzle (a_swz depends on r/4 mod
+        // 4), so they lie 32*BK bytes apart; B's 32-column block j of this
+        // wavefront's 128 columns sits (j/2) panels and (j%2)*32 columns past
+        // block 0.
+        const int ra0 = a_lds_off(a_r0, kgrp), ra1 = a_lds_off(a_r0, kgrp + 1);
+        const int rb = T::A_BYTES + b_off_lds[0] + kgrp * 1024;
         auto frag = [&](u4 (&f)[NF][2], int q) -> u4 & {
             const int blk = q >> 1;
             return f[blk == 0 ? 0 : blk <= 4 ? WM + blk - 1 : blk - 4][q & 1];
         };
         const int wave_u = __builtin_amdgcn_readfirstlane(wave);
         auto read = [&](u4 (&f)[NF][2], const uint8_t *st, int q) {
-            frag(f, q) = *reinterpret_cast<const u4 *>(st + roff[q]);
+            const int blk = q >> 1, c = q & 1;
+            const uint8_t *p = blk >= 1 && blk <= 4
+                                   ? st + rb + ((blk - 1) >> 1) * (CPR * 1024) + ((blk - 1) & 1) * 512 + c * 1024
+                                   : st + (c ? ra1 : ra0) + (blk == 0 ? 0 : (blk - 4) * 32 * BK);
+            frag(f, q) = *reinterpret_cast<const u4 *>(p);
         };
         // load l (A blocks, then B) of step lt into the stage at `lst`
         auto load = [&](uint8_t *lst, int lt, int l, bool checked) {
