@@ -123,7 +123,10 @@ def test_epilogue_activation(dev, kernel, act):
 @pytest.mark.parametrize("kernel", ["mfma", "skinny", "valu", "mfma_128"])
 @pytest.mark.parametrize("act", [capi.ACT_NONE, capi.ACT_GELU_ERF])
 def test_bf16_output_is_rne_of_fp32(dev, kernel, act):
-    """bf16 output is bit-exactly bf16_rne of the same kernel's fp32 output."""
+    """bf16 output is bit-exactly bf16_rne of the same kernel's fp32 output.
+    For the 256x256 tile kernel (N = 448) the two outputs come from different
+    layouts -- bf16 from 2x2 wavefronts of 128x128, fp32 from 2x4 of 128x64
+    -- so this also checks that both layouts sum in the same order."""
     M = 16 if not kernel.startswith("mfma") else 384
     c = make_case(M, 448, 1024, seed=13, dev=dev)
     bias = make_bias("N", M, 448, seed=4)
@@ -164,7 +167,9 @@ def test_mfma_epilogue_layouts(dev, kernel, layout, out_dtype, N):
     the output is aligned and C does not vary over rows) and a general one;
     both give the same bits, write nothing outside the [M, N] view, and
     match the oracle.  The reference is the same kernel into a dense fp32
-    output (bf16: its bf16_rne)."""
+    output (bf16: its bf16_rne); for the 256x256 kernels with N > 256 a bf16
+    output takes the one-wavefront-per-SIMD layout and fp32 the 2x4 one, so
+    the bf16 cases also compare the two layouts bit for bit."""
     M = 300
     c = make_case(M, N, 512, seed=N + 11, dev=dev)
     bias = make_bias("N", M, N, seed=5)
