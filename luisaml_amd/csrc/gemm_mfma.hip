@@ -548,8 +548,11 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         auto load = [&](uint8_t *lst, int lt, int l, bool checked) {
             const uint32_t kbyte = (uint32_t)lt * BK;
             if (l < T::A_BLK) {
-                uint32_t off = a_off[l] + kbyte;  // rows past M: OOB + kbyte, still out of range
-                if (checked) off = kbyte + (uint32_t)a_kc[l] < a_klim[l] ? off : OOB;
+                // rows past M carry OOB, and OOB + kbyte stays out of range;
+                // the lane's k-chunk a_kc is the same for every row block
+                // (a_swz of row (wave*A_BLK + l)*16 + lane/4 is (lane/16) % 4)
+                uint32_t off = a_off[l] + kbyte;
+                if (checked) off = kbyte + (uint32_t)a_kc[0] < (uint32_t)g.K ? off : OOB;
                 lds_load16(a_rsrc, lst + (wave_u * T::A_BLK + l) * 1024, off);
             } else {
                 lds_load16(b_rsrc, lst + T::A_BYTES + (wave_u * T::B_BLK + l - T::A_BLK) * 1024,
