@@ -1,10 +1,19 @@
-// gemm_mfma.hip -- large-M FP8 GEMM on gfx950 matrix cores.
+// gemm_mfma.hip -- large-M FP8 GEMM (and the implicit-im2col conv) on gfx950
+// matrix cores.
 //
 // Y[M,N] = epilogue( A[M,K] (E4M3, row-major) x B[K,N] (E4M3, packed panels) )
 //
-// Workgroup tile 256x256, K step 64, 512 threads = 8 wavefronts laid out
-// 2 (M) x 4 (N); each wavefront owns a 128x64 sub-tile = 4x2 blocks of
-// 32x32 fp32 accumulators (128 per lane).
+// Three workgroup layouts, K step 64 (BK):
+//   * 256x256 tiles, 512 threads = 8 wavefronts laid out 2 (M) x 4 (N), each
+//     owning 128x64 = 4x2 blocks of 32x32 fp32 accumulators; two wavefronts
+//     per SIMD; a 4-stage LDS ring (LCML_GEMM_STAGES).  fp32 outputs, grids of
+//     one tile column and the conv.
+//   * 256x256 tiles, 256 threads = 2x2 wavefronts of 128x128 (4x4 blocks, the
+//     256 accumulators per lane in AGPRs), one wavefront per SIMD, a 5-stage
+//     ring and an explicitly placed step schedule.  bf16 outputs on grids of
+//     more than one tile column.
+//   * 128x128 tiles, 256 threads = 2x2 wavefronts of 64x64, two workgroups
+//     per CU, for mid-size GEMMs whose 256x256 grid would leave CUs idle.
 //
 // Two instantiations share everything but the matrix-core instruction:
 //   EXACT (default): the E4M3 fragments read from LDS are widened to bf16 in
@@ -12,26 +21,28 @@
 //     v_mfma_f32_32x32x16_bf16, which accumulates at fp32 accuracy.  Every
 //     product of two E4M3 values is exact in fp32, so the result differs from
 //     the fp32 reference only by summation order.
-//   FAST: v_mfma_f32_32x32x64_f8f6f4 directly on the E4M3 bytes.  Twice the
-//     matrix-core rate, but gfx950's FP8 MFMAs drop product bits more than
+//   native FP8: v_mfma_f32_32x32x64_f8f6f4 directly on the E4M3 bytes.  Twice
+//     the matrix-core rate, but gfx950's FP8 MFMAs drop product bits more than
 //     about 2^13 below the largest product of each block (measured: relative
 //     Frobenius error ~1.4e-5 on N(0,1) data), so it is an opt-in kernel.
-// A ring of LCML_GEMM_STAGES (4) LDS stages of one 64-k step each (A 16 KB +
-// B 16 KB for the 256x256 tile).  Tiles move global -> LDS with
-// buffer_load_dwordx4 ... lds (no staging registers): each wavefront
-// instruction deposits one contiguous 1 KB block, lanes whose offset is out
-// of range (rows >= M, k >= K, panels beyond N) deposit zeros.  While the
-// matrix cores work on one stage, the next three K steps stream into the
-// others; one barrier per K step.
+// Every layout sums each output's products in the same order, so all of them
+// give bit-identical results.
+//
+// Each LDS stage holds one 64-k step: A (BM x 64 B) then B (BN x 64 B), 32 KB
+// for a 256x256 tile.  Tiles move global -> LDS with buffer_load_dwordx4 ...
+// lds (no staging registers): each wavefront instruction deposits one
+// contiguous 1 KB block, and lanes whose offset is out of range (rows >= M,
+// k >= K, panels beyond N) deposit zeros.  While the matrix cores work on one
+// stage, the following K steps stream into the others; one barrier per step.
 //
 // LDS layouts (bank-conflict free for 16-lane groups of ds_read_b128 on the
 // 64-bank gfx950 LDS):
-//   A: row-major [256 rows][128 B]; the 16-byte chunk c of row r is stored
-//      at chunk position c ^ ((r >> 1) & 7).  A 1 KB load block is 8 rows;
-//      lane l fills position l%8 of row l/8, so it fetches logical chunk
-//      (l%8) ^ ((row >> 1) & 7) -- each 8-lane group still reads one
-//      contiguous 128 B row segment.
-//   B: the packed global layout verbatim, [4 panels][8 k-chunks][64 cols][16 B].
+//   A: row-major [rows][64 B]; the 16-byte chunk c of row r is stored at
+//      chunk position c ^ ((r >> 2) & 3).  A 1 KB load block is 16 rows;
+//      lane l fills position l%4 of row l/4, so it fetches logical chunk
+//      (l%4) ^ ((row >> 2) & 3) -- each 4-lane group still reads one
+//      contiguous 64 B row segment.
+//   B: the packed global layout verbatim, [panels][4 k-chunks][64 cols][16 B].
 // MFMA operand chunks: lane l of a 32x32x64 fragment holds row/column l%32
 // and k = (l/32)*32 + 0..31, i.e. two consecutive 16-byte k-chunks.
 //
