@@ -18,6 +18,29 @@ from tests.gemm_cases import assert_close
 pytestmark = pytest.mark.gpu
 
 
+def full_matrix_check(y, qa, sa, qb_kn, sb, bias=None, frob=None):
+    """Every element of y against a float32 GEMM of the dequantised operands
+    computed on the GPU by torch (A = to_float(qa) * sa, B = to_float(qb) *
+    sb, as DequantizeLinear does): |y - ref| <= 1e-4 * (|A| @ |B| + |bias|).
+    The sampled rows are checked against the oracle; this covers every tile
+    of the grid.  With frob, also the relative Frobenius error."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    A = qa.view(torch.float8_e4m3fn).float() * sa
+    B = qb_kn.view(torch.float8_e4m3fn).float() * sb
+    ref = A @ B
+    bound = A.abs() @ B.abs()
+    del A, B
+    if bias is not None:
+        ref += bias
+        bound += bias.abs()
+    err = (y.float() - ref).abs()
+    bad = int((~(err <= 1e-4 * bound)).sum())
+    assert bad == 0, f"{bad} elements outside 1e-4 * sum|ab|"
+    if frob is not None:
+        rel = float(torch.linalg.vector_norm(y.float() - ref) / torch.linalg.vector_norm(ref))
+        assert rel < frob, rel
+
+
 def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
@@ -83,6 +106,9 @@ def test_gemm_8192_cubed_sampled_rows(dev, cube_8192):
     n = 8192
     y = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.float32, kernel=capi.KERNEL_MFMA)
     assert_close(y[torch.from_numpy(ROWS).to(dev)].cpu().numpy(), ref, bound)
+    full_matrix_check(y, qa, sa, capi.unpack_weight(bp, n, n, w_is_nk=False), sb)
+    # the bf16 output comes from the other 256x256 layout (2x2 wavefronts of
+    # 128x128): bit for bit the rounding of the fp32 one on every element
     y16 = capi.gemm(qa, sa, bp, sb, n, n, out_dtype=torch.bfloat16, kernel=capi.KERNEL_MFMA)
     assert torch.equal(y16.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
 
@@ -97,6 +123,9 @@ def test_gemm_8192_cubed_native_fp8_sampled_rows(dev, cube_8192):
     assert np.all(np.abs(ys - ref) <= 1e-4 * bound)
     rel = np.linalg.norm(ys - ref) / np.linalg.norm(ref)
     assert rel < 3e-5, rel
+    full_matrix_check(y, qa, sa, capi.unpack_weight(bp, 8192, 8192, w_is_nk=False), sb, frob=3e-5)
+    y16 = capi.gemm(qa, sa, bp, sb, 8192, 8192, out_dtype=torch.bfloat16, kernel=capi.KERNEL_MFMA_FP8)
+    assert torch.equal(y16.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
 
 
 def test_transformer_up_projection_gelu_sampled_rows(dev):
@@ -144,6 +173,8 @@ def test_transformer_qkv_and_o_projection_sampled_rows(dev, block_input, name, i
     assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias))
     y16 = capi.gemm_dynamic(d_x, bp, d_sw, N, 4096, c=d_b, out_dtype=torch.bfloat16)
     assert torch.equal(y16.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
+    qx, sx = capi.quantize_dynamic(d_x)
+    full_matrix_check(y, qx.view(4096, 4096), sx, capi.unpack_weight(bp, 4096, N, w_is_nk=False), d_sw, bias=d_b)
 
 
 def test_transformer_down_projection_from_gelu_output(dev, block_input):
@@ -165,6 +196,9 @@ def test_transformer_down_projection_from_gelu_output(dev, block_input):
     assert s_out.cpu().numpy().view(np.uint32)[0] == sh_ref.view(np.uint32)
     ref, A, B = oracle.qlinear(oracle.quantize(h_host[rows], sh_ref), sh_ref, qw, sw, bias=bias)
     assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias))
+    qh, shd = capi.quantize_dynamic(h)
+    full_matrix_check(y, qh.view(4096, 11008), shd, capi.unpack_weight(bp, 11008, 4096, w_is_nk=False), d_sw,
+                      bias=to_dev(bias, dev))
 
 
 def test_conv3x3_resnet_one_image(dev):
