@@ -13,7 +13,7 @@ import torch
 
 import oracle
 from luisaml_amd import capi, synth
-from tests.gemm_cases import assert_close
+from tests.gemm_cases import assert_close, gelu_tol
 
 pytestmark = pytest.mark.gpu
 
@@ -142,6 +142,18 @@ def test_transformer_up_projection_gelu_sampled_rows(dev):
     ref, A, B = oracle.qlinear(oracle.quantize(x[rows], s_ref), s_ref, qw, sw, bias=bias, act=oracle.ACT_GELU_ERF)
     assert_close(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, oracle.gemm_abs_bound(A, B, bias),
                  act=oracle.ACT_GELU_ERF)
+    # every element: GELU (exact erf, torch) of a GPU fp32 GEMM of the
+    # dequantised operands, at the GELU tolerance of the oracle checks
+    qx, sx = capi.quantize_dynamic(to_dev(x, dev))
+    Ad = qx.view(torch.float8_e4m3fn).float() * sx
+    Bd = capi.unpack_weight(bp, 4096, 11008, w_is_nk=False).view(torch.float8_e4m3fn).float() * d_sw
+    d_b = to_dev(bias, dev)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    pre = Ad @ Bd + d_b
+    bound_all = Ad.abs() @ Bd.abs() + d_b.abs()
+    del Ad, Bd
+    bad = int((~((y - torch.nn.functional.gelu(pre)).abs() <= gelu_tol(oracle.ACT_GELU_ERF) * bound_all)).sum())
+    assert bad == 0, f"{bad} elements outside the GELU tolerance"
 
 
 @pytest.fixture(scope="module")
@@ -223,6 +235,20 @@ def test_conv3x3_resnet_one_image(dev):
     ref = oracle.conv2d(A, B, bias, pads=(1, 1), act=oracle.ACT_RELU)
     bound = oracle.conv2d(np.abs(A), np.abs(B), np.abs(bias), pads=(1, 1))
     assert_close(y[img:img + 1].cpu().numpy(), ref, bound, act=oracle.ACT_RELU)
+    # all 32 images against torch's fp32 direct conv of the dequantised
+    # operands on the GPU (MIOpen off: no Winograd transform in the reference)
+    xd = xq.view(torch.float8_e4m3fn).float().permute(0, 3, 1, 2).contiguous() * sx
+    wd = torch.from_numpy(B).to(dev)
+    d_b = to_dev(bias, dev)
+    cudnn = torch.backends.cudnn.enabled
+    torch.backends.cudnn.enabled = False
+    try:
+        ref_all = torch.relu(torch.nn.functional.conv2d(xd, wd, d_b, padding=1))
+        bound_all = torch.nn.functional.conv2d(xd.abs(), wd.abs(), d_b.abs(), padding=1)
+    finally:
+        torch.backends.cudnn.enabled = cudnn
+    bad = int((~((y - ref_all).abs() <= 1e-4 * bound_all)).sum())
+    assert bad == 0, f"{bad} conv outputs outside 1e-4 * sum|xw|"
 
 
 @pytest.mark.parametrize("M", [64, 256, 512])
