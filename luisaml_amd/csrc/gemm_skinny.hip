@@ -283,7 +283,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     float a_dyn = 1.0f;
     if constexpr (DYN) {
         __shared__ float wmax[WAVES];
+        __shared__ uint32_t wbad[WAVES];
         float m = 0.0f;
+        float nf = 0.0f;  // x * 0 summed: NaN once any x is NaN or +-inf
         for (uint32_t base = 0; base < nq; base += NT * UQ) {
             if (base) {
 #pragma unroll
@@ -295,27 +297,43 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
                 // in the standalone amax
                 const float ax = fabsf(v[u].x), ay = fabsf(v[u].y), az = fabsf(v[u].z), aw = fabsf(v[u].w);
                 m = ax > m ? ax : m; m = ay > m ? ay : m; m = az > m ? az : m; m = aw > m ? aw : m;
+                nf = fmaf(v[u].x, 0.0f, nf); nf = fmaf(v[u].y, 0.0f, nf);
+                nf = fmaf(v[u].z, 0.0f, nf); nf = fmaf(v[u].w, 0.0f, nf);
             }
         }
         for (int off = 32; off > 0; off >>= 1) {
             const float o = __shfl_xor(m, off, 64);
             m = o > m ? o : m;
         }
-        if (lane == 0) wmax[wave] = m;
+        const bool wave_bad = __builtin_amdgcn_ballot_w64(nf != nf) != 0;
+        if (lane == 0) {
+            wmax[wave] = m;
+            wbad[wave] = wave_bad ? 1u : 0u;
+        }
         __syncthreads();
         m = wmax[0];
+        uint32_t bad = wbad[0];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) m = wmax[w] > m ? wmax[w] : m;
+        for (int w = 1; w < WAVES; ++w) {
+            m = wmax[w] > m ? wmax[w] : m;
+            bad |= wbad[w];
+        }
         a_dyn = scale_from_amax_bits(f32_bits(m));
         if (g.scale_out && blockIdx.x == 0 && tid == 0) *g.scale_out = a_dyn;
         const Recip d = make_recip(a_dyn);
-        // the scale's range test is uniform: one branch outside the loops
-        auto encode_all = [&](auto fast) {
+        // the scale's range test and the NaN/inf test are uniform: one
+        // branch outside the loops (mode 2: fast scale and clean input, 1:
+        // fast scale, 0: IEEE division)
+        auto encode_all = [&](auto mode) {
             auto put = [&](uint32_t i, f4 x4) {
                 uint32_t r, c;
                 split(i, r, c);
-                reinterpret_cast<uint32_t *>(a_lds + r * pitch)[c] =
-                    quantize4_t<decltype(fast)::value>(x4.x, x4.y, x4.z, x4.w, d);
+                uint32_t code;
+                if constexpr (decltype(mode)::value == 2)
+                    code = quantize4_clean(x4.x, x4.y, x4.z, x4.w, d);
+                else
+                    code = quantize4_t<decltype(mode)::value == 1>(x4.x, x4.y, x4.z, x4.w, d);
+                reinterpret_cast<uint32_t *>(a_lds + r * pitch)[c] = code;
             };
             if (nq <= NT * UQ) {  // one round: the values are still in registers
 #pragma unroll
@@ -335,10 +353,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
                 }
             }
         };
-        if (d.fast)
-            encode_all(std::true_type{});
+        if (d.fast && !bad)
+            encode_all(std::integral_constant<int, 2>{});
+        else if (d.fast)
+            encode_all(std::integral_constant<int, 1>{});
         else
-            encode_all(std::false_type{});
+            encode_all(std::integral_constant<int, 0>{});
         const uint32_t zq = (uint32_t)(pitch - 16) / 4 - kq;  // zero words per row for K <= k < Kp
         for (uint32_t i = tid; i < (uint32_t)g.M * zq; i += NT) {
             const uint32_t r = i / zq;

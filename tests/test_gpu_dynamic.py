@@ -100,6 +100,34 @@ def test_fused_row_pitch_and_specials(dev):
     assert float(s_out.item()) == 1.0 and float(y.abs().max()) == 0.0
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("big", [448.0, 3.0e5, 2.0e13])
+def test_fused_finite_input_tiny_and_signed_zero_quotients(dev, M, big):
+    """Finite inputs (no NaN, no inf) take the fused kernel's lean encode;
+    its results equal the two-launch composition bit for bit, including
+    quotients below 2^-100 (subnormal and tiny normal x against a large
+    amax, which take the IEEE-division fallback), +-0, the smallest
+    subnormals, values at the amax and ties of the E4M3 grid."""
+    K, N = 1024, 320
+    rng = np.random.default_rng(int(big) % 1000 + M)
+    x = (rng.standard_normal((M, K)) * (big / 8.0)).astype(np.float32)
+    flat = x.reshape(-1)
+    specials = np.array([big, -big, 0.0, -0.0, 1e-40, -1e-40, 2.0 ** -149, -(2.0 ** -149), 1e-30, -1e-30,
+                         2.0 ** -100, -(2.0 ** -126), big * (1.0625 / 448.0), -big * (1.1875 / 448.0)], np.float32)
+    idx = rng.choice(flat.size, specials.size, replace=False)
+    flat[idx] = specials
+    qw, sw, bp, d_sw = weights(K, N, 11, dev)
+    x_d = to_dev(x, dev)
+    s_out = torch.empty(1, dtype=torch.float32, device=dev)
+    y = capi.gemm_dynamic(x_d, bp, d_sw, N, K, scale_out=s_out, kernel=capi.KERNEL_SKINNY)
+    y2, q2, s2 = two_step(x_d, bp, d_sw, N, K, capi.KERNEL_SKINNY)
+    torch.cuda.synchronize()
+    s_ref = np.float32(oracle.dynamic_scale(x))
+    assert s_out.cpu().numpy().view(np.uint32)[0] == s_ref.view(np.uint32)
+    assert np.array_equal(q2.cpu().numpy(), oracle.quantize(x, s_ref))
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+
+
 @pytest.mark.parametrize("M,kernel", [(64, capi.KERNEL_AUTO), (4, capi.KERNEL_MFMA), (300, capi.KERNEL_MFMA_FP8),
                                       (16, capi.KERNEL_VALU)])
 def test_workspace_path(dev, M, kernel):
