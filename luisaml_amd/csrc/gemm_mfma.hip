@@ -533,6 +533,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // gains) and on grids of one tile column it loses 3-6%; those keep
         // the 2x4 layout.
         constexpr int NF = WM + WN;
+        static_assert(NF == 8 && T::LOADS <= 14 && NSTAGE >= 4,
+                      "schedule: 16 chunk reads of 4+4 fragments, the loads on the MFMAs after the barrier");
         u4 f0[NF][2], f1[NF][2];  // raw E4M3 fragments [A0..A3, B0..B3][16-byte chunk]
         // The 16 chunk reads of a step, q = 0..15 in the order the first
         // MFMAs of a step use them: A0, B0..B3, A1..A3 (two chunks each).
