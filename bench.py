@@ -377,7 +377,8 @@ def main() -> int:
         except Exception as exc:
             out["library_reference"]["gemm_8192_error"] = f"{type(exc).__name__}: {str(exc)[:120]}"
         out["gemm_8192"] = {"workload": "8192^3 E4M3 x E4M3, per-tensor scales, fp32 accumulate, bf16 out",
-                            "default_kernel": "exact_bf16_mfma", **big,
+                            "default_kernel": "exact_bf16_mfma",
+                            "tile": "256x256, 2x2 wavefronts of 128x128 (one per SIMD), 5-stage LDS ring", **big,
                             "roofline": {"bound": "mfma", "achieved": big["exact_bf16_mfma"]["tflops"],
                                          "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                                          "frac": round(big["exact_bf16_mfma"]["tflops"] / FP8_PEAK_TFLOPS, 4)}}
