@@ -66,7 +66,11 @@ extern "C" {
  * gfx950's native FP8 MFMAs at twice the matrix-core rate, but those
  * instructions drop product bits more than ~2^13 below the largest product
  * of each block (relative Frobenius error ~1.4e-5 on N(0,1) data, above the
- * 1e-5 bar), so they are never picked by AUTO. */
+ * 1e-5 bar), so AUTO never picks them.  AUTO_FP8 is the opt-in: AUTO's
+ * choice of tiling, run with the native FP8 twin of that kernel (SKINNY ->
+ * SKINNY_FP8, MFMA -> MFMA_FP8, MFMA_128 -> MFMA_128_FP8), for callers that
+ * accept the FP8-MFMA precision for twice the large-GEMM rate.  It has no
+ * counterpart in the reference, whose Gemm runs fp32 fma chains. */
 #define LCML_KERNEL_AUTO 0
 #define LCML_KERNEL_MFMA 1       /* 256x256 LDS double-buffered tiles, E4M3 widened to bf16 MFMA */
 #define LCML_KERNEL_SKINNY 2     /* small-M: weights streamed to registers, bf16 16x16x32 MFMA */
@@ -75,6 +79,7 @@ extern "C" {
 #define LCML_KERNEL_SKINNY_FP8 5 /* as SKINNY with v_mfma_f32_16x16x128_f8f6f4 */
 #define LCML_KERNEL_MFMA_128 6   /* as MFMA with 128x128 tiles (mid-size GEMMs) */
 #define LCML_KERNEL_MFMA_128_FP8 7 /* as MFMA_128 with v_mfma_f32_32x32x64_f8f6f4 */
+#define LCML_KERNEL_AUTO_FP8 8   /* AUTO's tiling with the native FP8 MFMA kernels (opt-in) */
 
 /* Message of the last failed call on this thread ("" if none). */
 LCML_API const char *lcml_fp8_last_error(void);
@@ -266,8 +271,9 @@ LCML_API int lcml_fp8_pack_conv_weight(const uint8_t *w, int64_t cout, int64_t c
  * w_packed: lcml_fp8_pack_conv_weight output.  bias: cout floats or NULL.
  * y: NCHW [n][cout][oh][ow], y_dtype LCML_DTYPE_FLOAT or BFLOAT16.
  * kernel: LCML_KERNEL_AUTO / MFMA / MFMA_128 (exact bf16 matrix cores,
- *    256x256 or 128x128 tiles) or MFMA_FP8 / MFMA_128_FP8; AUTO takes the
- *    128x128 tiles when the 256x256 grid (times the groups) is small.
+ *    256x256 or 128x128 tiles) or MFMA_FP8 / MFMA_128_FP8 / AUTO_FP8; AUTO
+ *    takes the 128x128 tiles when the 256x256 grid (times the groups) is
+ *    small, AUTO_FP8 the same tiles with the native FP8 MFMAs.
  * Replaces Conv::apply (src/onnx/operators/conv.cpp:115-207) for the
  * DQ(x), DQ(W) -> Conv [-> Relu/Gelu] pattern.
  */

@@ -22,6 +22,7 @@ BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_MFMA, KERNEL_SKINNY, KERNEL_VALU, KERNEL_MFMA_FP8, KERNEL_SKINNY_FP8 = 0, 1, 2, 3, 4, 5
 KERNEL_MFMA_128, KERNEL_MFMA_128_FP8 = 6, 7
+KERNEL_AUTO_FP8 = 8  # AUTO's tiling with the native FP8 MFMA kernels (opt-in)
 DYNAMIC_WORKSPACE_BYTES = 4096
 DYNAMIC_SMALL_MAX = 65536
 PACK_K, PANEL_COLS = 128, 64

@@ -160,6 +160,16 @@ namespace {
 // tiles keeps the 256x256 kernel.  Examples: 4096x11008 at M = 512: 128x128
 // tiles 64 us against 83 (skinny) and 93 (256x256); 4096x4096 at M = 1024:
 // 46 us against 66 and 91; 11008x4096 at M = 512: skinny 73 us against 91.
+// the native-FP8 kernel of the same tiling (LCML_KERNEL_AUTO_FP8)
+int fp8_twin(int kernel) {
+    switch (kernel) {
+    case LCML_KERNEL_MFMA: return LCML_KERNEL_MFMA_FP8;
+    case LCML_KERNEL_MFMA_128: return LCML_KERNEL_MFMA_128_FP8;
+    case LCML_KERNEL_SKINNY: return LCML_KERNEL_SKINNY_FP8;
+    default: return kernel;
+    }
+}
+
 int auto_gemm_kernel(int64_t M, int64_t N, int64_t K) {
     if (M <= 16) return LCML_KERNEL_SKINNY;
     const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
@@ -192,6 +202,7 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
     hipStream_t s = (hipStream_t)stream;
     if (kernel == LCML_KERNEL_AUTO) kernel = auto_gemm_kernel(M, N, K);
+    if (kernel == LCML_KERNEL_AUTO_FP8) kernel = fp8_twin(auto_gemm_kernel(M, N, K));
     hipError_t err;
     switch (kernel) {
     case LCML_KERNEL_MFMA:
@@ -233,7 +244,7 @@ constexpr int64_t kAutoFuseMaxElems = 16384;
 bool dynamic_fusable(int64_t M, int64_t K, const float *x, int64_t ldx, int kernel) {
     const bool fits = M <= 16 && lcml::skinny_dynamic_lds_bytes(M, K) <= lcml::kSkinnyDynLdsMax &&
                       (!x || aligned(x, 16)) && ldx % 4 == 0 && ((M - 1) * ldx + K) * 4 < (int64_t)0x80000000;
-    if (kernel == LCML_KERNEL_AUTO) return fits && M * K <= kAutoFuseMaxElems;
+    if (kernel == LCML_KERNEL_AUTO || kernel == LCML_KERNEL_AUTO_FP8) return fits && M * K <= kAutoFuseMaxElems;
     return fits && (kernel == LCML_KERNEL_SKINNY || kernel == LCML_KERNEL_SKINNY_FP8);
 }
 int64_t pad256(int64_t n) { return (n + 255) / 256 * 256; }
@@ -272,7 +283,9 @@ int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const flo
     hipStream_t s = (hipStream_t)stream;
     if (dynamic_fusable(M, K, x, ldx, kernel))
         return hip_status(lcml::launch_gemm_skinny_dynamic(M, N, K, x, ldx, b_packed, e, x_scale_out,
-                                                           kernel != LCML_KERNEL_SKINNY_FP8, s),
+                                                           kernel != LCML_KERNEL_SKINNY_FP8 &&
+                                                               kernel != LCML_KERNEL_AUTO_FP8,
+                                                           s),
                           fn);
     // two-step path: quantise into the workspace, then the selected GEMM.
     // The size is that of this path whatever the size query said: the query
@@ -417,17 +430,19 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
     if (n * h * w * c >= (int64_t)1 << 31 || M >= (int64_t)1 << 31 ||
         lcml_fp8_packed_conv_weight_bytes(cout, c / group, kh, kw, group) >= (int64_t)1 << 31)
         return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB", fn);
-    if (kernel == LCML_KERNEL_AUTO) {
+    if (kernel == LCML_KERNEL_AUTO || kernel == LCML_KERNEL_AUTO_FP8) {
         // as auto_gemm_kernel without the skinny kernel; groups add grid rows
         const int64_t N = cout / group;
         const double big = (double)((M + 255) / 256 * ((N + 255) / 256) * group);
         const double t128 = (double)((M + 127) / 128 * ((N + 127) / 128) * group);
         const double small = 2.2 * (t128 > 256 ? t128 / 256 : 1.0);
-        kernel = big < 256 && small < 4.5 ? LCML_KERNEL_MFMA_128 : LCML_KERNEL_MFMA;
+        const int tiles = big < 256 && small < 4.5 ? LCML_KERNEL_MFMA_128 : LCML_KERNEL_MFMA;
+        kernel = kernel == LCML_KERNEL_AUTO_FP8 ? fp8_twin(tiles) : tiles;
     }
     if (kernel != LCML_KERNEL_MFMA && kernel != LCML_KERNEL_MFMA_FP8 && kernel != LCML_KERNEL_MFMA_128 &&
         kernel != LCML_KERNEL_MFMA_128_FP8)
-        return fail(LCML_ERR_UNSUPPORTED, "%s: kernel %d (AUTO or one of the MFMA tile kernels)", fn, kernel);
+        return fail(LCML_ERR_UNSUPPORTED, "%s: kernel %d (AUTO, AUTO_FP8 or one of the MFMA tile kernels)", fn,
+                    kernel);
     lcml::Epilogue e;
     if (int rc = make_epilogue(e, fn, M, cout, x_scale, w_scale, w_scale_per_channel, 1.0f, bias, 1, cout, 0, 1.0f,
                                act, y, y_dtype, cout))

@@ -71,6 +71,7 @@ class NetworkInstance {
     const uint8_t *weight_buffer_ = nullptr;  // device
     size_t weight_bytes_ = 0;
     bool fusion_ = true;
+    bool fp8_mfma_ = false;
     bool memory_planning_ = true;
     bool prepared_ = false;
     MemoryPlan plan_;
@@ -100,6 +101,11 @@ public:
     void set_output(std::string_view name, ITensor &t);
     // QDQ -> FP8Linear fusion (default on); off runs every node as written.
     void set_fusion(bool on) { fusion_ = on; }
+    // Fused FP8Linear / FP8Conv nodes on gfx950's native FP8 matrix-core
+    // instructions (LCML_KERNEL_AUTO_FP8: twice the large-GEMM rate, FP8-MFMA
+    // precision) instead of the exact kernels (default off).  Set before
+    // prepare(); no reference counterpart.
+    void set_fp8_matrix_cores(bool on) { fp8_mfma_ = on; }
     // Intermediates share one arena by live range (default on); off gives
     // every intermediate its own allocation.
     void set_memory_planning(bool on) { memory_planning_ = on; }

@@ -287,6 +287,7 @@ void NetworkInstance::fuse_qdq_linear() {
             f.set_attribute(Attribute{"a_mode", (int32_t)aq.a_mode});
             f.set_attribute(Attribute{"has_bias", (int32_t)has_bias});
             f.set_attribute(Attribute{"act", (int32_t)act});
+            f.set_attribute(Attribute{"fp8_mfma", (int32_t)fp8_mfma_});
             f.set_attribute(Attribute{"weight", W.get_name()});
             for (size_t d : drop) removed[d] = true;
             replacement.emplace(i, std::move(f));
@@ -377,6 +378,7 @@ void NetworkInstance::fuse_qdq_linear() {
         f.set_attribute(Attribute{"beta", gemm ? attr_float(n, "beta", 1.0f) : 1.0f});
         f.set_attribute(Attribute{"w_is_nk", (int32_t)w_is_nk});
         f.set_attribute(Attribute{"trans_a", (int32_t)trans_a});
+        f.set_attribute(Attribute{"fp8_mfma", (int32_t)fp8_mfma_});
         f.set_attribute(Attribute{"weight", W.get_name()});
         if (!wbatch.empty()) f.set_attribute(Attribute{"wbatch", wbatch});
         for (size_t d : drop) removed[d] = true;

@@ -121,12 +121,14 @@ public:
 class FP8Conv : public StreamOperator {
     ConvAttrs attrs_;
     int a_mode_, has_bias_, act_;
+    int kernel_;  // LCML_KERNEL_AUTO, or AUTO_FP8 (NetworkInstance::set_fp8_matrix_cores)
     std::unique_ptr<DeviceBuffer> xq_, sx_, ws_;
     size_t xq_bytes_ = 0;
 
 public:
-    FP8Conv(ConvAttrs a, int a_mode, int has_bias, int act)
-        : StreamOperator("FP8Conv"), attrs_(std::move(a)), a_mode_(a_mode), has_bias_(has_bias), act_(act) {}
+    FP8Conv(ConvAttrs a, int a_mode, int has_bias, int act, int kernel)
+        : StreamOperator("FP8Conv"), attrs_(std::move(a)), a_mode_(a_mode), has_bias_(has_bias), act_(act),
+          kernel_(kernel) {}
     void forward(std::span<std::reference_wrapper<ITensor>> inputs,
                  std::span<std::reference_wrapper<ITensor>> outputs) override {
         ITensor &X = inputs[0], &Y = outputs[0];
@@ -163,7 +165,7 @@ public:
         }
         check(lcml_fp8_conv2d(xq, sx, n, c, h, w, W->packed(), W->scale(), W->per_channel(), Y.shape(1), a_.kh, a_.kw,
                               a_.sh, a_.sw, a_.ph, a_.pw, a_.dh, a_.dw, attrs_.group, oh, ow, bias, act_,
-                              Y.device_data(), out_dtype_code(Y, "FP8Conv"), LCML_KERNEL_AUTO, stream_),
+                              Y.device_data(), out_dtype_code(Y, "FP8Conv"), kernel_, stream_),
               "FP8Conv");
     }
 };
@@ -173,7 +175,8 @@ public:
 REGISTER_TO_DEFAULT_OPSET(Conv) { return std::make_unique<Conv>(conv_attrs(node)); };
 REGISTER_TO_DEFAULT_OPSET(FP8Conv) {
     return std::make_unique<FP8Conv>(conv_attrs(node), attr_int(node, "a_mode", 2),
-                                     attr_int(node, "has_bias", 0), attr_int(node, "act", 0));
+                                     attr_int(node, "has_bias", 0), attr_int(node, "act", 0),
+                                     attr_int(node, "fp8_mfma", 0) ? LCML_KERNEL_AUTO_FP8 : LCML_KERNEL_AUTO);
 };
 
 }  // namespace lcml::onnx

@@ -144,6 +144,7 @@ class FP8Linear : public StreamOperator {
     int a_mode_, has_c_, act_, trans_a_;
     float alpha_, beta_;
     std::vector<int32_t> wbatch_;
+    int kernel_;  // LCML_KERNEL_AUTO, or AUTO_FP8 (NetworkInstance::set_fp8_matrix_cores)
     std::unique_ptr<DeviceBuffer> qa_, ws_, sx_;
     size_t qa_bytes_ = 0, ws_bytes_ = 0;
 
@@ -223,16 +224,17 @@ class FP8Linear : public StreamOperator {
                       "FP8Linear");
             else
                 check(lcml_fp8_gemm(M, N, K, q + ao, K, sa_dev, W.packed(bo), W.scale(), W.per_channel(), alpha_,
-                                    nullptr, 0, 0, 0, beta_, act_, yt, ydt, N, LCML_KERNEL_AUTO, stream_),
+                                    nullptr, 0, 0, 0, beta_, act_, yt, ydt, N, kernel_, stream_),
                       "FP8Linear");
             for (int d = nb - 1; d >= 0 && ++idx[d] == ydim[d]; --d) idx[d] = 0;
         }
     }
 
 public:
-    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta, int trans_a, std::vector<int32_t> wbatch)
+    FP8Linear(int a_mode, int has_c, int act, float alpha, float beta, int trans_a, std::vector<int32_t> wbatch,
+              int kernel)
         : StreamOperator("FP8Linear"), a_mode_(a_mode), has_c_(has_c), act_(act), trans_a_(trans_a), alpha_(alpha),
-          beta_(beta), wbatch_(std::move(wbatch)) {}
+          beta_(beta), wbatch_(std::move(wbatch)), kernel_(kernel) {}
     void forward(std::span<std::reference_wrapper<ITensor>> inputs,
                  std::span<std::reference_wrapper<ITensor>> outputs) override {
         ITensor &A = inputs[0], &Y = outputs[0];
@@ -279,7 +281,7 @@ public:
                 sa = static_cast<const float *>(sx_->data());
             }
             check(lcml_fp8_gemm(M, N, K, q, K, sa, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
-                                c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, LCML_KERNEL_AUTO, stream_),
+                                c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, kernel_, stream_),
                   "FP8Linear");
             return;
         }
@@ -296,14 +298,14 @@ public:
             // takes the two-step path (the MFMA kernel's size)
             const bool a16 = (reinterpret_cast<uintptr_t>(a) & 15) == 0;
             const int64_t ws =
-                lcml_fp8_gemm_dynamic_workspace_bytes(M, K, a16 ? LCML_KERNEL_AUTO : LCML_KERNEL_MFMA);
+                lcml_fp8_gemm_dynamic_workspace_bytes(M, K, a16 ? kernel_ : LCML_KERNEL_MFMA);
             if (ws > 0 && (!ws_ || ws_bytes_ < (size_t)ws)) {
                 ws_ = std::make_unique<DeviceBuffer>((size_t)ws);
                 ws_bytes_ = (size_t)ws;
             }
             check(lcml_fp8_gemm_dynamic(M, N, K, a, K, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim,
                                         c.d0, c.d1, beta_, act_, Y.device_data(), ydt, N, nullptr,
-                                        ws > 0 ? ws_->data() : nullptr, ws, LCML_KERNEL_AUTO, stream_),
+                                        ws > 0 ? ws_->data() : nullptr, ws, kernel_, stream_),
                   "FP8Linear");
             return;
         }
@@ -317,7 +319,7 @@ public:
         const float *sa = static_cast<const float *>(a_scale->device_data());
         check(lcml_fp8_quantize(a, q, 1, 1, M * K, sa, stream_), "FP8Linear quantize");
         check(lcml_fp8_gemm(M, N, K, q, K, sa, W->packed(), W->scale(), W->per_channel(), alpha_, c.ptr, c.ndim, c.d0,
-                            c.d1, beta_, act_, Y.device_data(), ydt, N, LCML_KERNEL_AUTO, stream_),
+                            c.d1, beta_, act_, Y.device_data(), ydt, N, kernel_, stream_),
               "FP8Linear");
     }
 };
@@ -339,7 +341,8 @@ REGISTER_TO_DEFAULT_OPSET(FP8Linear) {
     return std::make_unique<FP8Linear>(attr_int(node, "a_mode", 0), attr_int(node, "has_c", 0),
                                        attr_int(node, "act", 0), attr_float(node, "alpha", 1.0f),
                                        attr_float(node, "beta", 1.0f), attr_int(node, "trans_a", 0),
-                                       attr_ints(node, "wbatch", {}));
+                                       attr_ints(node, "wbatch", {}),
+                                       attr_int(node, "fp8_mfma", 0) ? LCML_KERNEL_AUTO_FP8 : LCML_KERNEL_AUTO);
 };
 
 }  // namespace lcml::onnx

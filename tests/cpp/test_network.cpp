@@ -1442,6 +1442,118 @@ static void test_conv1d(bool fused) {
     CHECK(close(y, ref, bound, 1e-4, 0.0, "conv1d"));
 }
 
+// NetworkInstance::set_fp8_matrix_cores: the fused FP8Linear runs gfx950's
+// native FP8 MFMA kernels (LCML_KERNEL_AUTO_FP8).  Static QDQ (scale 1)
+// activation -> MatMul(DQ(W), scale 1) with one row pattern 1, 2^-7 and one
+// column pattern 1, 2^-7: the exact kernels return 1 + 2^-14, the FP8 MFMAs
+// drop the product 14 binades below the largest (1.0), on the skinny (M = 1)
+// and the tile (M = 1024) paths.  Then the dynamic QDQ MatMul on N(0,1) data
+// against the oracle: the elementwise summation-order bound and relative
+// Frobenius error < 3e-5 (the FP8-MFMA truncation), and not bit-identical to
+// the exact network.
+static std::vector<float> run_fp8_matmul(const std::vector<float> &x, const std::vector<uint8_t> &qw, int M, int K,
+                                         int N, bool dynamic, bool fp8_mfma, const std::vector<float> &sw) {
+    std::vector<uint8_t> zp(1, 0);
+    const float one = 1.0f;
+    Graph g("fp8mfma");
+    Blob blob;
+    var(g, "x", DataType::FLOAT, {(size_t)M, (size_t)K});
+    blob_var(g, blob, "W", DataType::FLOAT8E4M3FN, {(size_t)K, (size_t)N}, qw.data(), qw.size());
+    blob_var(g, blob, "sw", DataType::FLOAT, {(size_t)N}, sw.data(), N * 4);
+    var(g, "xq", DataType::FLOAT8E4M3FN, {(size_t)M, (size_t)K});
+    var(g, "xd", DataType::FLOAT, {(size_t)M, (size_t)K});
+    var(g, "Wf", DataType::FLOAT, {(size_t)K, (size_t)N});
+    var(g, "y", DataType::FLOAT, {(size_t)M, (size_t)N});
+    if (dynamic) {
+        var(g, "xs", DataType::FLOAT, {1});
+        var(g, "xz", DataType::FLOAT8E4M3FN, {1});
+        node(g, "DynamicQuantizeLinear", {"x"}, {"xq", "xs", "xz"});
+    } else {
+        raw_var(g, "xs", DataType::FLOAT, {1}, &one, 4);
+        raw_var(g, "xz", DataType::FLOAT8E4M3FN, {1}, zp.data(), 1);
+        node(g, "QuantizeLinear", {"x", "xs", "xz"}, {"xq"});
+    }
+    node(g, "DequantizeLinear", {"xq", "xs", "xz"}, {"xd"});
+    node(g, "DequantizeLinear", {"W", "sw"}, {"Wf"}, {Attribute{"axis", (int32_t)1}});
+    node(g, "MatMul", {"xd", "Wf"}, {"y"});
+    g.add_input("x");
+    g.add_output("y");
+    Model m(10, "test", "1");
+    m.set_graph(std::move(g));
+    DeviceBuffer wb(blob.bytes.size());
+    CHECK(hipMemcpy(wb.data(), blob.bytes.data(), blob.bytes.size(), hipMemcpyHostToDevice) == hipSuccess);
+    auto xt = upload(x, {(uint32_t)M, (uint32_t)K});
+    auto yt = make_device_tensor<float>({(uint32_t)M, (uint32_t)N});
+    NetworkInstance net;
+    net.set_fp8_matrix_cores(fp8_mfma);
+    net.set_model(std::move(m));
+    net.set_weight_buffer(wb.data(), blob.bytes.size());
+    net.set_input("x", *xt);
+    net.set_output("y", *yt);
+    net.forward();
+    CHECK(net.fused_linear_count() == 1 && net.executed_op_types().size() == 1u);
+    return download<float>(*yt);
+}
+
+static void test_fp8_matrix_cores() {
+    std::printf("[19] set_fp8_matrix_cores: fused FP8Linear on the native FP8 MFMA kernels\n");
+    {
+        const int K = 128, N = 64;
+        std::vector<uint8_t> qw((size_t)K * N, 0);
+        for (int n = 0; n < N; ++n) {
+            qw[n] = 0x38;          // 1.0
+            qw[(size_t)N + n] = 0x04;  // 2^-7
+        }
+        const std::vector<float> sw(N, 1.0f);
+        for (int M : {1, 1024}) {
+            std::vector<float> x((size_t)M * K, 0.0f);
+            for (int r = 0; r < M; ++r) {
+                x[(size_t)r * K] = 1.0f;
+                x[(size_t)r * K + 1] = 0x1p-7f;
+            }
+            auto exact = run_fp8_matmul(x, qw, M, K, N, false, false, sw);
+            auto fast = run_fp8_matmul(x, qw, M, K, N, false, true, sw);
+            bool ok = true;
+            for (size_t i = 0; i < exact.size(); ++i) ok &= exact[i] == 1.0f + 0x1p-14f && fast[i] == 1.0f;
+            if (!ok) std::printf("  M=%d: expected 1 + 2^-14 (exact) and 1 (FP8 MFMA), got %a and %a\n", M,
+                                 (double)exact[0], (double)fast[0]);
+            CHECK(ok);
+        }
+    }
+    {
+        const int M = 512, K = 1024, N = 1024;
+        auto x = normals(191, (size_t)M * K, 1.0f), w = normals(192, (size_t)K * N, 0.02f);
+        std::vector<float> sw(N, 0.0f);
+        for (int k = 0; k < K; ++k)
+            for (int n = 0; n < N; ++n) sw[n] = std::max(sw[n], std::fabs(w[(size_t)k * N + n]));
+        for (auto &s : sw) s = orc_scale_from_amax(s);
+        std::vector<uint8_t> qw(w.size());
+        orc_quantize(w.data(), qw.data(), K, N, 1, sw.data());
+        auto exact = run_fp8_matmul(x, qw, M, K, N, true, false, sw);
+        auto fast = run_fp8_matmul(x, qw, M, K, N, true, true, sw);
+        float sx = orc_scale_from_amax(orc_amax(x.data(), x.size()));
+        std::vector<uint8_t> qx(x.size());
+        orc_quantize(x.data(), qx.data(), 1, 1, x.size(), &sx);
+        std::vector<float> A(x.size()), Bw(w.size()), ref((size_t)M * N);
+        orc_dequantize(qx.data(), A.data(), 1, 1, qx.size(), &sx);
+        orc_dequantize(qw.data(), Bw.data(), K, N, 1, sw.data());
+        orc_gemm(M, N, K, A.data(), 0, Bw.data(), 0, 1.0f, 0.0f, nullptr, -1, 0, 0, 0, ref.data());
+        std::vector<double> bound((size_t)M * N);
+        orc_gemm_abs_bound(M, N, K, A.data(), 0, Bw.data(), 0, 1.0f, 0.0f, nullptr, -1, 0, 0, bound.data());
+        CHECK(close(exact, ref, bound, 1e-4, 0.0, "exact network"));
+        CHECK(close(fast, ref, bound, 1e-4, 0.0, "FP8-MFMA network"));
+        double num = 0, den = 0;
+        for (size_t i = 0; i < ref.size(); ++i) {
+            num += ((double)fast[i] - ref[i]) * ((double)fast[i] - ref[i]);
+            den += (double)ref[i] * ref[i];
+        }
+        const double rel = std::sqrt(num / den);
+        std::printf("  relative Frobenius error of the FP8-MFMA network: %.3g\n", rel);
+        CHECK(rel < 3e-5);
+        CHECK(exact != fast);
+    }
+}
+
 int main(int argc, char **argv) {
     if (argc < 2) {
         std::printf("usage: test_network <golden dir>\n");
@@ -1479,6 +1591,7 @@ int main(int argc, char **argv) {
         test_gemm_trans_a(true);
         test_conv1d(false);
         test_conv1d(true);
+        test_fp8_matrix_cores();
         test_errors();
     } catch (const Error &e) {
         std::printf("FAIL: uncaught error: %s\n", e.what());

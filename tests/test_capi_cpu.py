@@ -35,7 +35,8 @@ def test_abi_version():
 
 def test_python_constants_match_header():
     assert capi.DYNAMIC_WORKSPACE_BYTES == header_define("LCML_FP8_DYNAMIC_WORKSPACE_BYTES")
-    for name in ("AUTO", "MFMA", "SKINNY", "VALU", "MFMA_FP8", "SKINNY_FP8", "MFMA_128", "MFMA_128_FP8"):
+    for name in ("AUTO", "MFMA", "SKINNY", "VALU", "MFMA_FP8", "SKINNY_FP8", "MFMA_128", "MFMA_128_FP8",
+                 "AUTO_FP8"):
         assert getattr(capi, "KERNEL_" + name) == header_define("LCML_KERNEL_" + name), name
 
 
@@ -127,7 +128,7 @@ def _gemm_dynamic(M, K, x, ldx, ws, ws_bytes, kernel=0, N=64):
                                             0x1000, 1, N, None, ws, ws_bytes, kernel, None)
 
 
-@pytest.mark.parametrize("kernel", [capi.KERNEL_AUTO, capi.KERNEL_SKINNY])
+@pytest.mark.parametrize("kernel", [capi.KERNEL_AUTO, capi.KERNEL_SKINNY, capi.KERNEL_AUTO_FP8])
 def test_dynamic_gemm_misaligned_x_needs_the_two_step_workspace(kernel):
     """A 4-byte-aligned x cannot take the fused kernel, so the call quantises
     into the workspace: the size query (which assumes an aligned x) says 0
@@ -161,3 +162,22 @@ def test_noalloc_dynamic_gemm_rejects_oversize_before_any_launch():
     # M == 0: nothing to do, no scratch needed
     assert L.lcml_fp8_gemm_dynamic_noalloc(0, 64, K, None, K, None, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
                                            0x1000, 1, 64, None, 0, None) == capi.OK
+
+
+def test_auto_fp8_is_accepted_where_auto_is():
+    """LCML_KERNEL_AUTO_FP8 sizes the dynamic workspace as AUTO does (fused
+    at small M*K, two-step otherwise), and the conv entry point takes it as
+    a tile-kernel choice: with a batch of 0 images the call validates
+    everything and returns before any launch."""
+    L = capi.lib()
+    for M, K in ((1, 4096), (4, 4096), (16, 4096), (64, 4096)):
+        assert (L.lcml_fp8_gemm_dynamic_workspace_bytes(M, K, capi.KERNEL_AUTO_FP8)
+                == L.lcml_fp8_gemm_dynamic_workspace_bytes(M, K, capi.KERNEL_AUTO)), (M, K)
+
+    def conv(kernel):
+        return L.lcml_fp8_conv2d(0x1000, 0x1000, 0, 32, 8, 8, 0x1000, 0x1000, 0, 16, 3, 3, 1, 1, 1, 1, 1, 1, 1,
+                                 8, 8, None, 0, 0x1000, 1, kernel, None)
+
+    assert conv(capi.KERNEL_AUTO) == capi.OK
+    assert conv(capi.KERNEL_AUTO_FP8) == capi.OK
+    assert conv(capi.KERNEL_SKINNY) == capi.ERR_UNSUPPORTED and "AUTO_FP8" in capi.last_error()

@@ -315,3 +315,66 @@ def test_concurrent_streams_match_serial(dev):
         torch.cuda.synchronize()
         for i in range(5):
             assert torch.equal(outs[i].view(torch.int32), serial[i].view(torch.int32)), (rep, i)
+
+
+EXACT_TO_FP8 = {capi.KERNEL_MFMA: capi.KERNEL_MFMA_FP8, capi.KERNEL_MFMA_128: capi.KERNEL_MFMA_128_FP8,
+                capi.KERNEL_SKINNY: capi.KERNEL_SKINNY_FP8}
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 2048, 1024), (40, 1024, 1024), (512, 1024, 1024), (2048, 4096, 512)])
+def test_auto_fp8_runs_the_fp8_twin_of_autos_choice(dev, M, N, K):
+    """LCML_KERNEL_AUTO_FP8 takes AUTO's tiling with the native FP8 MFMAs:
+    its bits are those of the FP8 twin of the exact kernel whose bits AUTO
+    reproduces (the skinny kernel at small M, 128x128 or 256x256 tiles
+    above), and it stays within the FP8-MFMA bounds of the oracle."""
+    c = make_case(M, N, K, seed=M + 3 * N + K, dev=dev)
+    auto = run(c, capi.KERNEL_AUTO, dev=dev)
+    picked = [k for k in EXACT_TO_FP8 if torch.equal(run(c, k, dev=dev).view(torch.int32), auto.view(torch.int32))]
+    assert picked, "AUTO matches none of the exact kernels"
+    fast = run(c, capi.KERNEL_AUTO_FP8, dev=dev)
+    assert any(torch.equal(fast.view(torch.int32), run(c, EXACT_TO_FP8[k], dev=dev).view(torch.int32))
+               for k in picked)
+    y = fast.cpu().numpy().astype(np.float64)
+    ref, bound = reference(c)
+    assert np.all(np.abs(y - ref) <= 1e-4 * bound)
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 3e-5
+
+
+@pytest.mark.parametrize("M", [1, 4, 64])
+def test_auto_fp8_dynamic(dev, M):
+    """gemm_dynamic with AUTO_FP8: the fused skinny FP8 kernel where AUTO
+    fuses (M*K <= 16384), else quantise + the AUTO_FP8 GEMM; bit-identical
+    to the two launches written out."""
+    N, K = 2048, 4096
+    c = make_case(M, N, K, seed=70 + M, dev=dev)
+    x = torch.from_numpy(synth.normal(71 + M, (M, K))).to(dev)
+    got = capi.gemm_dynamic(x, c.d_bp, c.d_sb, N, K, kernel=capi.KERNEL_AUTO_FP8)
+    qx, sx = capi.quantize_dynamic(x)
+    want = capi.gemm(qx, sx, c.d_bp, c.d_sb, N, K, kernel=capi.KERNEL_SKINNY_FP8 if M * K <= 16384
+                     else capi.KERNEL_AUTO_FP8)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_auto_fp8_conv(dev):
+    """conv2d with AUTO_FP8 gives the bits of the native-FP8 tile kernel of
+    AUTO's tile size."""
+    n, cin, h, w, cout = 4, 64, 28, 28, 128
+    x = torch.from_numpy(synth.normal(81, (n, cin, h, w))).to(dev)
+    wt = synth.normal(82, (cout, cin, 3, 3), std=0.05)
+    sw = oracle.channel_scales(wt, axis=0)
+    d_sw = torch.from_numpy(sw).to(dev)
+    qw = torch.from_numpy(oracle.quantize(wt, sw, axis=0)).to(dev)
+    bp = capi.pack_conv_weight(qw)
+    xq, sx = capi.quantize_nhwc(x)
+    args = dict(kernel_shape=(3, 3), pads=(1, 1))
+    auto = capi.conv2d(xq, sx, bp, d_sw, cout, kernel=capi.KERNEL_AUTO, **args)
+    fast = capi.conv2d(xq, sx, bp, d_sw, cout, kernel=capi.KERNEL_AUTO_FP8, **args)
+    for exact, fp8 in ((capi.KERNEL_MFMA, capi.KERNEL_MFMA_FP8), (capi.KERNEL_MFMA_128, capi.KERNEL_MFMA_128_FP8)):
+        if torch.equal(capi.conv2d(xq, sx, bp, d_sw, cout, kernel=exact, **args).view(torch.int32),
+                       auto.view(torch.int32)):
+            assert torch.equal(capi.conv2d(xq, sx, bp, d_sw, cout, kernel=fp8, **args).view(torch.int32),
+                               fast.view(torch.int32))
+            break
+    else:
+        pytest.fail("AUTO matches neither tile kernel")
+    assert not torch.equal(fast.view(torch.int32), auto.view(torch.int32))
