@@ -30,6 +30,9 @@ EXACT = {"mfma": capi.KERNEL_MFMA, "mfma_128": capi.KERNEL_MFMA_128, "skinny": c
          "valu": capi.KERNEL_VALU, "auto": capi.KERNEL_AUTO}
 NATIVE = {"mfma_fp8": capi.KERNEL_MFMA_FP8, "mfma_128_fp8": capi.KERNEL_MFMA_128_FP8,
           "skinny_fp8": capi.KERNEL_SKINNY_FP8}
+# the opt-in AUTO_FP8 (AUTO's tiling on the native FP8 kernels): drawn in
+# cases of its own, so the draws of the cases above stay as they were
+OPT_IN = {"auto_fp8": capi.KERNEL_AUTO_FP8}
 FP8_FROB = 3e-5
 ACTS = [capi.ACT_NONE, capi.ACT_RELU, capi.ACT_GELU_ERF, capi.ACT_GELU_TANH]
 C_KINDS = [None, "N", "1", "scalar", "M1", "MN", "1N", "M"]
@@ -97,7 +100,7 @@ def check(y, ref, bound, p):
     if not p["bf16"]:
         nr = np.linalg.norm(ref)
         rel = np.linalg.norm(y - ref) / nr if nr > 0 else np.linalg.norm(y)
-        lim = FP8_FROB if p["kname"] in NATIVE else TOL_FROB
+        lim = FP8_FROB if p["kname"] in NATIVE or p["kname"] in OPT_IN else TOL_FROB
         assert rel <= lim, f"{p}: relative Frobenius error {rel:.3e} > {lim}"
 
 
@@ -122,7 +125,7 @@ def oracle_out(qa, sa, qw, sw, C, p):
 
 def run_case(p, dev, dynamic):
     M, N, K = p["M"], p["N"], p["K"]
-    kernel = {**EXACT, **NATIVE}[p["kname"]]
+    kernel = {**EXACT, **NATIVE, **OPT_IN}[p["kname"]]
     print(f"case {p}", flush=True)
     x = synth.normal(p["seed"] + 1, (M, K), std=p["a_std"])
     sa = np.float32(oracle.dynamic_scale(x))
@@ -189,7 +192,26 @@ def draw_conv(i):
 def test_random_conv(dev, i):
     """Implicit-im2col FP8 conv (NHWC E4M3 in, NCHW out) against the oracle's
     direct conv of the dequantised operands (conv.cpp:115-207)."""
-    p = draw_conv(i)
+    run_conv(draw_conv(i), dev)
+
+
+@pytest.mark.parametrize("i", range(48))
+def test_random_gemm_auto_fp8(dev, i):
+    """LCML_KERNEL_AUTO_FP8 through lcml_fp8_gemm (two cases in three) and
+    lcml_fp8_gemm_dynamic, at the native-FP8 bars."""
+    p = draw_case(5000 + i)
+    p["kname"] = "auto_fp8"
+    run_case(p, dev, dynamic=i % 3 == 0)
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_conv_auto_fp8(dev, i):
+    p = draw_conv(6000 + i)
+    p["kname"] = "auto_fp8"
+    run_conv(p, dev)
+
+
+def run_conv(p, dev):
     print(f"case {p}", flush=True)
     n, c, h, w, cout, kh, kw, g = p["n"], p["c"], p["h"], p["w"], p["cout"], p["kh"], p["kw"], p["group"]
     st, pd, dl = (p["stride"],) * 2, (p["pad"],) * 2, (p["dil"],) * 2
@@ -217,7 +239,7 @@ def test_random_conv(dev, i):
     capi.conv2d(xq, d_sx, capi.pack_conv_weight(torch.from_numpy(qw).to(dev), group=g),
                 torch.from_numpy(ws).to(dev), cout, (kh, kw), st, pd, dl,
                 bias=None if bias is None else torch.from_numpy(bias).to(dev), act=p["act"],
-                kernel=CONV_KERNELS[p["kname"]], out=out, group=g)
+                kernel={**CONV_KERNELS, **OPT_IN}[p["kname"]], out=out, group=g)
     torch.cuda.synchronize()
     assert d_sx.cpu().numpy().view(np.uint32)[0] == sx.view(np.uint32)
     check(out, ref, bound, p)
