@@ -378,9 +378,11 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         }
 #pragma unroll
         for (int i = 0; i < T::B_BLK; ++i) {
-            // steps past the end (the pipeline tail) load whatever lies there
-            // into a stage that is never read again
-            const uint32_t off = b_off[i] != OOB ? b_off[i] + (uint32_t)kt * CPR * 1024 : OOB;
+            // steps past the end (the pipeline tail) still issue their loads,
+            // so that every step counts the same loads for the vmcnt waits,
+            // but out of range: zeros into a stage that is never read again,
+            // no memory traffic
+            const uint32_t off = b_off[i] != OOB && kt < g.nk ? b_off[i] + (uint32_t)kt * CPR * 1024 : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 b_rsrc, (lds_void *)(sa + T::A_BYTES + (wave * T::B_BLK + i) * 1024), 16, off, 0, 0, 0);
         }
@@ -573,8 +575,10 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 if (checked) off = kbyte + (uint32_t)a_kc[0] < (uint32_t)g.K ? off : OOB;
                 lds_load16(a_rsrc, lst + (wave_u * T::A_BLK + l) * 1024, off);
             } else {
+                // past the last step (checked steps only): out of range, as in issue_tile
+                const uint32_t boff = b_off[l - T::A_BLK] + (uint32_t)lt * CPR * 1024;
                 lds_load16(b_rsrc, lst + T::A_BYTES + (wave_u * T::B_BLK + l - T::A_BLK) * 1024,
-                           b_off[l - T::A_BLK] + (uint32_t)lt * CPR * 1024);
+                           checked && lt >= g.nk ? OOB : boff);
             }
         };
         auto sync_step = [&]() {
