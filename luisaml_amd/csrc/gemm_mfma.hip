@@ -164,9 +164,11 @@ __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) 
 // exact).  bf16 pairs are packed by v_cvt_pk_bf16_f32, which rounds to
 // nearest even exactly as bf16_rne does (checked over all 2^32 fp32 inputs).
 // Every store is a buffer store, and the hardware drops those past the
-// buffer's extent: a row past M lies past num_records = M * ldy elements and
-// a lane whose columns lie past N carries an offset past it (the caller
-// keeps (M + 64) * ldy elements below 2^31 bytes, so no offset wraps).
+// buffer's extent: a row past M lies past num_records = M * ldy elements, and
+// a lane whose columns lie past N, or a pass that starts past M, carries an
+// offset past it.  The caller keeps (M + 64) * ldy elements below 2^31 bytes,
+// so neither a pass that starts before M (rows up to M + 62) nor OOB plus 31
+// row steps of a pass past M wraps 32 bits.
 // With every CU busy, the general path (uniform tests on every element,
 // software rounding) took ~19 us for a 256x256 tile's bf16 epilogue, this one
 // ~4.5 us (fp32: ~8 us); on the 4096-row transformer linears that is 6-7% of
@@ -181,7 +183,7 @@ __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, in
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(e.y, 0, (int)(e.M * e.ldy * ES), 0x00020000);
     const uint32_t step = (uint32_t)(2 * e.ldy * ES);
-    uint32_t off = cols_ok ? (uint32_t)((row0 * e.ldy + col) * ES) : OOB;
+    uint32_t off = cols_ok && row0 < e.M ? (uint32_t)((row0 * e.ldy + col) * ES) : OOB;
     const float alpha = e.alpha;
 #pragma unroll 8
     for (int q = 0; q < 32; ++q, off += step) {

@@ -202,6 +202,30 @@ def test_mfma_epilogue_layouts(dev, kernel, layout, out_dtype, N):
     assert bool((buf.cpu()[mask.cpu()] == fill).all())
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "mfma_128", "mfma_fp8"])
+@pytest.mark.parametrize("out_dtype,ldy", [(torch.bfloat16, 9_000_000), (torch.float32, 4_500_000)])
+@pytest.mark.parametrize("M", [1, 17])
+def test_mfma_epilogue_huge_row_pitch(dev, kernel, out_dtype, ldy, M):
+    """A few rows with a ~18 MB row pitch: (M + 64) rows of pitch stay below
+    2^31 bytes, so the specialised row-major epilogue runs, while the tile's
+    256 staged rows reach ~4.6e9 bytes.  A pass of staged rows past M must
+    store nothing (its 32-bit offsets would otherwise wrap into row 0's
+    pitch padding); the view gets the same bits as a dense output and every
+    other element of the buffer keeps its fill."""
+    N = 320
+    c = make_case(M, N, 512, seed=M + 101, dev=dev)
+    ref = run(c, KERNELS[kernel], out_dtype=out_dtype, dev=dev)
+    fill = -12288.0  # exact in bf16
+    buf = torch.full((M * ldy,), fill, dtype=out_dtype, device=dev)
+    view = buf.as_strided((M, N), (ldy, 1))
+    capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, out=view, kernel=KERNELS[kernel])
+    torch.cuda.synchronize()
+    assert torch.equal(view.view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32),
+                       ref.view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32))
+    view.fill_(fill)
+    assert int((buf != fill).sum().item()) == 0
+
+
 def test_kernels_agree_small_m(dev):
     """All three kernels on one decode-shaped case agree within the bound."""
     c = make_case(16, 2048, 4096, seed=21, dev=dev)
