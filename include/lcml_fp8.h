@@ -84,6 +84,15 @@ extern "C" {
 /* Message of the last failed call on this thread ("" if none). */
 LCML_API const char *lcml_fp8_last_error(void);
 
+/* Names of the kernels this thread launched since the previous call, comma
+ * separated in launch order ("gemm_skinny_dynamic", "quantize_dynamic,
+ * gemm_mfma_256", ...; entry points that launch fixed kernels are named
+ * after themselves), then the record is cleared.  The string stays valid
+ * until the thread's next call of this function.  No counterpart in the
+ * reference (whose GPU code has no C ABI); the operator layer's execution
+ * log (NetworkInstance::enable_logging) reads it per node. */
+LCML_API const char *lcml_fp8_kernel_trace(void);
+
 /* LCML_FP8_ABI_VERSION of the loaded library. */
 LCML_API int lcml_fp8_abi_version(void);
 

@@ -39,6 +39,7 @@ _lib = None
 _vp, _i64, _int, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
 _SIGS = {
     "lcml_fp8_last_error": (C.c_char_p, []),
+    "lcml_fp8_kernel_trace": (C.c_char_p, []),
     "lcml_fp8_abi_version": (_int, []),
     "lcml_fp8_quantize": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "lcml_fp8_dequantize": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
@@ -98,6 +99,12 @@ def lib():
 
 def last_error() -> str:
     return lib().lcml_fp8_last_error().decode()
+
+
+def kernel_trace() -> list[str]:
+    """Kernels launched on this thread since the previous call, in order."""
+    t = lib().lcml_fp8_kernel_trace().decode()
+    return t.split(", ") if t else []
 
 
 def _check(rc: int) -> None:

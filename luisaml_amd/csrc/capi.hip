@@ -3,6 +3,7 @@
 // synchronises the host or allocates device memory.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <atomic>
 
@@ -12,6 +13,19 @@
 namespace {
 
 thread_local char g_err[512] = "";
+// names of the kernels launched on this thread since the last
+// lcml_fp8_kernel_trace() call, comma separated (truncated when full)
+thread_local char g_trace[1024] = "";
+thread_local char g_trace_out[1024] = "";
+thread_local size_t g_trace_len = 0;
+
+void note(const char *label) {
+    const size_t n = strlen(label), sep = g_trace_len ? 2 : 0;
+    if (g_trace_len + sep + n + 1 > sizeof(g_trace)) return;
+    if (sep) memcpy(g_trace + g_trace_len, ", ", 2);
+    memcpy(g_trace + g_trace_len + sep, label, n + 1);
+    g_trace_len += sep + n;
+}
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -21,8 +35,13 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
-int hip_status(hipError_t err, const char *what) {
-    if (err == hipSuccess) return LCML_OK;
+// a launch's status; on success the launch is noted in the kernel trace
+// under `label` (the entry point's name when none is given)
+int hip_status(hipError_t err, const char *what, const char *label = nullptr) {
+    if (err == hipSuccess) {
+        note(label ? label : what);
+        return LCML_OK;
+    }
     return fail(LCML_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
 }
 
@@ -80,6 +99,13 @@ int make_epilogue(lcml::Epilogue &e, const char *fn, int64_t M, int64_t N, const
 extern "C" {
 
 const char *lcml_fp8_last_error(void) { return g_err; }
+
+const char *lcml_fp8_kernel_trace(void) {
+    memcpy(g_trace_out, g_trace, g_trace_len + 1);
+    g_trace[0] = 0;
+    g_trace_len = 0;
+    return g_trace_out;
+}
 
 int lcml_fp8_abi_version(void) { return LCML_FP8_ABI_VERSION; }
 
@@ -170,6 +196,20 @@ int fp8_twin(int kernel) {
     }
 }
 
+// the kernel trace's name of a resolved GEMM kernel choice
+const char *kernel_label(int kernel) {
+    switch (kernel) {
+    case LCML_KERNEL_MFMA: return "gemm_mfma_256";
+    case LCML_KERNEL_MFMA_FP8: return "gemm_mfma_256_fp8";
+    case LCML_KERNEL_MFMA_128: return "gemm_mfma_128";
+    case LCML_KERNEL_MFMA_128_FP8: return "gemm_mfma_128_fp8";
+    case LCML_KERNEL_SKINNY: return "gemm_skinny";
+    case LCML_KERNEL_SKINNY_FP8: return "gemm_skinny_fp8";
+    case LCML_KERNEL_VALU: return "gemv_valu";
+    default: return "gemm";
+    }
+}
+
 int auto_gemm_kernel(int64_t M, int64_t N, int64_t K) {
     if (M <= 16) return LCML_KERNEL_SKINNY;
     const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
@@ -204,6 +244,7 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     if (kernel == LCML_KERNEL_AUTO) kernel = auto_gemm_kernel(M, N, K);
     if (kernel == LCML_KERNEL_AUTO_FP8) kernel = fp8_twin(auto_gemm_kernel(M, N, K));
     hipError_t err;
+    const char *label = kernel_label(kernel);
     switch (kernel) {
     case LCML_KERNEL_MFMA:
     case LCML_KERNEL_MFMA_FP8:
@@ -231,7 +272,7 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     case LCML_KERNEL_VALU: err = lcml::launch_gemv_valu_fp8(M, N, K, a, lda, b_packed, e, s); break;
     default: return fail(LCML_ERR_INVALID_ARG, "%s: unknown kernel %d", fn, kernel);
     }
-    return hip_status(err, fn);
+    return hip_status(err, fn, label);
 }
 
 namespace {
@@ -286,7 +327,10 @@ int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const flo
                                                            kernel != LCML_KERNEL_SKINNY_FP8 &&
                                                                kernel != LCML_KERNEL_AUTO_FP8,
                                                            s),
-                          fn);
+                          fn,
+                          kernel == LCML_KERNEL_SKINNY_FP8 || kernel == LCML_KERNEL_AUTO_FP8
+                              ? "gemm_skinny_dynamic_fp8"
+                              : "gemm_skinny_dynamic");
     // two-step path: quantise into the workspace, then the selected GEMM.
     // The size is that of this path whatever the size query said: the query
     // cannot see x, and a misaligned x takes this path where an aligned one
@@ -301,7 +345,7 @@ int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const flo
     uint32_t *part = reinterpret_cast<uint32_t *>(ws + pad256(M * K));
     float *scale = x_scale_out ? x_scale_out : reinterpret_cast<float *>(ws + pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
     hipError_t err = lcml::launch_quantize_dynamic(x, q, M * K, scale, part, s);
-    if (err != hipSuccess) return hip_status(err, fn);
+    if (int rc = hip_status(err, fn, "quantize_dynamic")) return rc;
     return lcml_fp8_gemm(M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
                          c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
 }
@@ -461,7 +505,11 @@ int lcml_fp8_conv2d(const uint8_t *x_nhwc, const float *x_scale, int64_t n, int6
                                              kernel == LCML_KERNEL_MFMA || kernel == LCML_KERNEL_MFMA_128,
                                              (hipStream_t)stream,
                                              kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8),
-                      fn);
+                      fn,
+                      kernel == LCML_KERNEL_MFMA       ? "conv_mfma_256"
+                      : kernel == LCML_KERNEL_MFMA_FP8 ? "conv_mfma_256_fp8"
+                      : kernel == LCML_KERNEL_MFMA_128 ? "conv_mfma_128"
+                                                       : "conv_mfma_128_fp8");
 }
 
 int lcml_fp8_gemm_w8a32(int64_t M, int64_t N, int64_t K, const float *a, int64_t lda, const uint8_t *b_packed,

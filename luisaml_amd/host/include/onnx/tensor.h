@@ -57,6 +57,7 @@ class DeviceArray {
     size_t byte_offset_ = 0;
     size_t count_ = 0;
     bool view_ = false;
+    mutable std::string name_;
 
 public:
     using value_type = T;
@@ -82,6 +83,10 @@ public:
           count_(count), view_(true) {}
 
     size_t size() const noexcept { return count_; }
+    // a debug name for the storage (ITensor::set_name forwards here); the
+    // reference names its DynamicArray storage the same way
+    void set_name(std::string_view name) const { name_ = name; }
+    const std::string &name() const noexcept { return name_; }
     bool is_byte_buffer() const noexcept { return true; }
     void *get_byte_buffer() const noexcept { return base_; }
     size_t get_byte_offset() const noexcept { return byte_offset_; }
@@ -117,6 +122,8 @@ public:
     virtual size_type size() const noexcept = 0;
     virtual refl::TypeIndex element_type_index() const noexcept = 0;
     virtual std::string_view element_type_name() const noexcept = 0;
+    // names the tensor's storage (reference tensor.h:128); no-op by default
+    virtual void set_name(std::string_view) const noexcept {}
     virtual bool is_constant() const noexcept { return false; }
     virtual bool is_view() const noexcept { return false; }
     virtual bool is_local() const noexcept { return false; }
@@ -161,6 +168,15 @@ public:
     std::string_view element_type_name() const noexcept override { return type_name_v<T>; }
     bool is_view() const noexcept override { return data_.is_view(); }
     void *device_data() const noexcept override { return data_.data(); }
+    // forwards to the container where it can hold a name (tensor.h:344-349)
+    void set_name(std::string_view name) const noexcept override {
+        if constexpr (requires { data_.set_name(name); }) {
+            try {
+                data_.set_name(name);
+            } catch (...) {
+            }
+        }
+    }
     Container &container() noexcept { return data_; }
     const Container &container() const noexcept { return data_; }
     T *data() const noexcept { return data_.data(); }

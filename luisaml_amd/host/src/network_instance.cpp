@@ -3,6 +3,7 @@
 #include "onnx/network_instance.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <unordered_map>
 #include <unordered_set>
@@ -42,11 +43,11 @@ void NetworkInstance::set_weight_buffer(const void *device_blob, size_t bytes) {
 }
 
 void NetworkInstance::set_input(std::string_view name, ITensor &t) {
-    inputs_.emplace_back(std::string(name), std::ref(t));
+    inputs_.insert_or_assign(std::string(name), std::ref(t));
 }
 
 void NetworkInstance::set_output(std::string_view name, ITensor &t) {
-    outputs_.emplace_back(std::string(name), std::ref(t));
+    outputs_.insert_or_assign(std::string(name), std::ref(t));
 }
 
 // Dtype and shape of an external tensor must match the graph variable
@@ -409,6 +410,8 @@ void NetworkInstance::pack_weights() {
         create_tensor_for_var(sw);
         // [batch dimensions..., K, N]: one packed weight per batch
         const auto &psh = pv.get_shape();
+        LCML_ASSERT(psh.size() >= 2, "%s: packed weight %s of rank %zu", n.get_op_type().c_str(),
+                    pv.get_name().c_str(), psh.size());
         const uint32_t K = (uint32_t)psh[psh.size() - 2], N = (uint32_t)psh[psh.size() - 1];
         uint32_t batches = 1;
         for (size_t d = 0; d + 2 < psh.size(); ++d) batches *= (uint32_t)psh[d];
@@ -431,8 +434,8 @@ void NetworkInstance::pack_weights() {
                            "pack weight");
         ITensor &st = table_.at(sw.get_name());
         DeviceArray<float> scale(static_cast<float *>(st.device_data()), 0, st.size());
-        table_.own(pv.get_name(),
-                   std::make_unique<PackedWeightTensor>(K, N, std::move(packed), std::move(scale), batches));
+        table_.own(pv.get_name(), std::make_unique<PackedWeightTensor>(to_tensor_shape(psh), std::move(packed),
+                                                                        std::move(scale)));
     }
 }
 
@@ -499,13 +502,82 @@ void NetworkInstance::forward() {
     for (auto &[name, t] : inputs_) table_.bind(name, t.get());
     for (auto &[name, t] : outputs_) table_.bind(name, t.get());
     const auto &nodes = g.get_nodes();
+    if (enable_logging_) {
+        log_graph();
+        (void)lcml_fp8_kernel_trace();  // start each node's record empty
+    }
     for (size_t i = 0; i < nodes.size(); ++i) {
         std::vector<std::reference_wrapper<ITensor>> ins, outs;
         for (auto &v : nodes[i].get_inputs()) ins.emplace_back(table_.at(v.get().get_name()));
         for (auto &v : nodes[i].get_outputs()) outs.emplace_back(table_.at(v.get().get_name()));
         ops_[i]->set_environment(*this, table_);
         ops_[i]->forward(ins, outs);
+        if (enable_logging_) log_node(i, nodes[i], lcml_fp8_kernel_trace());
     }
+}
+
+namespace {
+
+std::string shape_text(const std::vector<size_t> &shape) {
+    std::string s = "[";
+    for (size_t i = 0; i < shape.size(); ++i) s += (i ? ", " : "") + std::to_string(shape[i]);
+    return s + "]";
+}
+
+// a markdown table cell: '|' escaped
+std::string cell(std::string s) {
+    for (size_t p = 0; (p = s.find('|', p)) != std::string::npos; p += 2) s.replace(p, 1, "\\|");
+    return s;
+}
+
+std::string names(const std::vector<std::reference_wrapper<const Variable>> &vars) {
+    std::string s;
+    for (auto &v : vars) s += (s.empty() ? "" : ", ") + v.get().get_name();
+    return s.empty() ? "(none)" : s;
+}
+
+}  // namespace
+
+// The execution log's graph part, appended once per forward(): a summary
+// table and one row per node (index, operator, inputs, outputs) of the graph
+// as it executes, i.e. after QDQ fusion.
+void NetworkInstance::log_graph() const {
+    FILE *f = fopen(log_path_.c_str(), "a");
+    if (!f) return;
+    const Graph &g = model_.get_graph();
+    const auto &nodes = g.get_nodes();
+    fprintf(f, "\n# Network Execution Log\n\n## Summary\n\n| Metric | Value |\n|--------|-------|\n");
+    fprintf(f, "| Total Nodes | %zu |\n| Graph Inputs | %zu |\n| Graph Outputs | %zu |\n| Variables | %zu |\n",
+            nodes.size(), g.get_inputs().size(), g.get_outputs().size(), g.get_variables().size());
+    fprintf(f, "| Fused FP8 nodes | %zu |\n| Warp size | %u |\n\n", fused_count_, warp_size_);
+    fprintf(f, "## Nodes Detail\n\n| Index | Op Type | Inputs | Outputs |\n|-------|---------|--------|---------|\n");
+    for (size_t i = 0; i < nodes.size(); ++i)
+        fprintf(f, "| %zu | %s | %s | %s |\n", i, nodes[i].get_op_type().c_str(),
+                cell(names(nodes[i].get_inputs())).c_str(), cell(names(nodes[i].get_outputs())).c_str());
+    fprintf(f, "\n");
+    fclose(f);
+}
+
+// One executed node: its inputs and outputs with shapes and dtypes, and the
+// kernels its forward() launched (the C ABI's kernel trace).
+void NetworkInstance::log_node(size_t i, const Node &n, const char *kernels) const {
+    FILE *f = fopen(log_path_.c_str(), "a");
+    if (!f) return;
+    const size_t total = model_.get_graph().get_nodes().size();
+    fprintf(f, "\n### Node [%zu/%zu]: %s\n\n**Inputs:**\n", i, total - 1, n.get_op_type().c_str());
+    auto vars = [&](const std::vector<std::reference_wrapper<const Variable>> &vs) {
+        for (auto &v : vs) {
+            const std::string_view dt = data_type_name(v.get().get_dtype());
+            fprintf(f, "- `%s` : shape=%s, dtype=%.*s\n", v.get().get_name().c_str(),
+                    shape_text(v.get().get_shape()).c_str(), (int)dt.size(), dt.data());
+        }
+        if (vs.empty()) fprintf(f, "- (none)\n");
+    };
+    vars(n.get_inputs());
+    fprintf(f, "\n**Outputs:**\n");
+    vars(n.get_outputs());
+    fprintf(f, "\n**Kernels:** %s\n\n---\n", kernels && *kernels ? kernels : "(none)");
+    fclose(f);
 }
 
 std::vector<std::string> NetworkInstance::executed_op_types() const {

@@ -4,6 +4,7 @@
 // the imported nodes, the tensor API and the error behaviour.
 //   usage: test_registry <tests/golden dir>
 #include <algorithm>
+#include <concepts>
 #include <cstdio>
 #include <fstream>
 #include <sstream>
@@ -237,6 +238,96 @@ int main(int argc, char **argv) {
     });
     CHECK(visited == 1);
     CHECK(throws([] { visit_type_index<NNTypeList>(12345, []<typename T>() {}); }));
+    // set_name reaches the storage (tensor.h:128, 344-349 of the reference)
+    t.set_name("activations");
+    CHECK(t.container().name() == "activations");
+    static_cast<const ITensor &>(t).set_name("renamed");
+    CHECK(t.container().name() == "renamed");
+
+    // ---- TensorTable: ownership, parent fallback, release, iteration ----
+    {
+        float d1[4], d2[4], d3[4];
+        Tensor<float> ext({4}, DeviceArray<float>(d1, 0, 4));
+        TensorTable parent, child;
+        parent.own("w", std::make_unique<Tensor<float>>(ITensor::shape_type{4}, DeviceArray<float>(d2, 0, 4)));
+        child.bind("x", ext);
+        child.own("h", std::make_unique<Tensor<float>>(ITensor::shape_type{4}, DeviceArray<float>(d3, 0, 4)));
+        CHECK(!child.contains("w") && child.parent() == nullptr);
+        child.set_parent(&parent);
+        CHECK(child.parent() == &parent && child.contains("w") && !child.contains_local("w"));
+        CHECK(child.at("w").device_data() == d2 && &child.at("x") == &ext);
+        const TensorTable &cc = child;
+        CHECK(cc.at("h").device_data() == d3);
+        CHECK(child.entry("x").is_borrowed() && child.entry("h").is_owned() && !child.entry("h").is_borrowed());
+        CHECK(throws([&] { (void)child.entry("w"); }));          // entry() is local only
+        CHECK(throws([&] { (void)child.at("missing"); }));
+        CHECK(child.release_owned("x") == nullptr && child.contains_local("x"));  // borrowed stays
+        auto h = child.release_owned("h");
+        CHECK(h && h->device_data() == d3 && !child.contains("h") && child.size() == 1 && !child.empty());
+        size_t n = 0;
+        for (auto &[name, entry] : child) n += name == "x" && &entry.get() == &ext;
+        CHECK(n == 1);
+        child.clear();
+        CHECK(child.empty() && child.contains("w"));  // the parent keeps its entries
+    }
+
+    // ---- the reference's engine and table members exist with compatible
+    //      signatures (include/onnx/network_instance.h:185-230,
+    //      tensor_table.h:97-214, tensor.h:128) ----
+    {
+        static_assert(requires(NetworkInstance &n, const NetworkInstance &cn, ITensor &t, Model m) {
+            n.set_model(std::move(m));
+            n.set_input("x", t);
+            n.set_output("y", t);
+            n.set_warp_size(1u);
+            { cn.warp_size() } -> std::convertible_to<uint32_t>;
+            { cn.use_warp_optimization() } -> std::same_as<bool>;
+            n.set_use_cooperative_vector(true);
+            { cn.use_cooperative_vector() } -> std::same_as<bool>;
+            n.enable_logging(true);
+            { cn.get_model() } -> std::same_as<const Model &>;
+            cn.get_inputs().at("x").get();
+            cn.get_outputs().at("y").get();
+            { cn.get_tensor_table() } -> std::same_as<const TensorTable &>;
+            n.forward();
+        });
+        static_assert(requires(TensorTable &tt, const TensorTable &ct, ITensor &t) {
+            tt.set_parent(&tt);
+            { ct.parent() } -> std::same_as<TensorTable *>;
+            tt.bind("a", t);
+            tt.own("b", std::unique_ptr<ITensor>{});
+            { tt.at("a") } -> std::same_as<ITensor &>;
+            { ct.at("a") } -> std::same_as<const ITensor &>;
+            { ct.contains("a") } -> std::same_as<bool>;
+            { ct.contains_local("a") } -> std::same_as<bool>;
+            { tt.entry("a") } -> std::same_as<TensorEntry &>;
+            { ct.entry("a") } -> std::same_as<const TensorEntry &>;
+            { ct.size() } -> std::same_as<size_t>;
+            { ct.empty() } -> std::same_as<bool>;
+            tt.clear();
+            { tt.release_owned("b") } -> std::same_as<std::unique_ptr<ITensor>>;
+            tt.begin(); tt.end(); ct.begin(); ct.end(); ct.cbegin(); ct.cend();
+        });
+        static_assert(requires(TensorEntry &e, const TensorEntry &ce) {
+            { ce.is_owned() } -> std::same_as<bool>;
+            { ce.is_borrowed() } -> std::same_as<bool>;
+            { e.get() } -> std::same_as<ITensor &>;
+            { ce.get() } -> std::same_as<const ITensor &>;
+            { e.release_owned() } -> std::same_as<std::unique_ptr<ITensor>>;
+        });
+        static_assert(requires(const ITensor &t) { t.set_name("n"); });
+        NetworkInstance net;  // no device work until prepare()/forward()
+        CHECK(net.warp_size() == 64 && net.use_warp_optimization() && !net.use_cooperative_vector());
+        net.set_warp_size(1);
+        net.set_use_cooperative_vector(true);
+        CHECK(net.warp_size() == 1 && !net.use_warp_optimization() && net.use_cooperative_vector());
+        float d[4];
+        Tensor<float> a({4}, DeviceArray<float>(d, 0, 4)), b({4}, DeviceArray<float>(d, 0, 4));
+        net.set_input("x", a);
+        net.set_input("x", b);  // a later binding replaces the earlier one
+        CHECK(net.get_inputs().size() == 1 && &net.get_inputs().at("x").get() == &b && net.get_outputs().empty());
+        CHECK(net.get_tensor_table().empty() && net.log_file() == "./stats.md");
+    }
 
     std::printf(failures ? "FAILED (%d)\n" : "PASS\n", failures);
     return failures ? 1 : 0;
