@@ -252,6 +252,176 @@ __device__ __forceinline__ void epi_cols(const Epilogue &e, const float *srow, v
     }
 }
 
+// The lane index, computed where it is used (v_mbcnt): the volatile asm
+// cannot be hoisted, so the persistent kernel's code between tiles holds no
+// per-lane value through the main loop, whose registers are all taken.
+__device__ __forceinline__ int lane_here() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// Direct-store epilogue of the persistent one-wavefront-per-SIMD GEMM (bf16
+// output, no LDS).  Its MFMAs run with the operands swapped (the B block
+// first), so of a 32x32 block a lane holds one output row, m = lane % 32,
+// at columns 8*(r/4) + 4*(lane/32) + r%4 for accumulator r.  Each value
+// gets epi_value_cv's operations in its order (acc * scale * alpha, + beta
+// * C, the activation; no contraction); pairs are rounded to bf16 by
+// v_cvt_pk_bf16_f32, and one v_permlane32_swap per two pairs trades the
+// column groups 8g+4.. (upper lanes) and 8(g+1).. (lower lanes), after
+// which lane l holds 8 consecutive columns 16h + 8*(l/32) of its row.  Per
+// pass of 32 rows x 64 columns these 16-byte pieces go to the wavefront's
+// part of a free LDS stage and come back as whole 128-byte row segments,
+// 8 rows per buffer store: full cache lines, where storing the pieces
+// straight from the registers (32 rows x 32 bytes per store) measured 4-5%
+// slower at 8192^3.  Rows past M and columns past N carry an out-of-range
+// offset (the caller
+// guarantees N % 8 == 0, ldy % 8 == 0, a 16-byte aligned y, M * ldy * 2 <
+// 2^31 bytes, and a C that does not vary over rows).  mr0 / nc0: the
+// wavefront's first output row and column.
+// The uniform inputs of epi_direct_bf16, read once per kernel: the
+// per-tensor scale product and a scalar C (reads inside the tile loop would
+// be vector loads waiting on every load in flight).
+struct DirectUniforms {
+    float a_s, s_uni, c_uni;
+    bool pc, c_vec;
+};
+
+// (each value passed through v_readfirstlane: uniform, so it lives in a
+// scalar register rather than taking one of the main loop's vector ones)
+__device__ inline float uniform_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
+__device__ inline DirectUniforms direct_uniforms(const Epilogue &e) {
+    DirectUniforms u;
+    u.a_s = uniform_f(e.a_scale ? e.a_scale[0] : 1.0f);
+    u.pc = e.b_scale && e.b_per_channel;
+    u.s_uni = uniform_f(e.b_scale && !u.pc ? u.a_s * e.b_scale[0] : u.a_s);  // epi_scale of a per-tensor scale
+    // C over N (a vector) or one value: the row-invariant broadcasts of epi_c
+    u.c_vec = e.c && !(e.c_ndim == 0 || (e.c_ndim == 1 && e.c0 == 1) || (e.c_ndim == 2 && e.c1 == 1));
+    u.c_uni = uniform_f(e.c && !u.c_vec ? e.c[0] : 0.0f);
+    return u;
+}
+
+// Row pitch (bytes) of the epilogue's per-wavefront LDS staging: 32 rows of
+// 64 bf16 columns plus 16 bytes, so the 16 rows of a ds_write_b128 lane group
+// fall on distinct 16-byte bank slots (9 slots per row, odd).
+constexpr int EPD_PITCH = 144;
+// a wavefront's part of the free ring stage: the staging rows, then its 128
+// columns' scales and C (512 bytes each, each the first half of a 1 KB
+// global->LDS load whose upper lanes load nothing)
+constexpr int EPD_SCALE = 32 * EPD_PITCH, EPD_C = EPD_SCALE + 1024, EPD_BYTES = EPD_C + 1024;
+
+// ALPHA1: alpha == 1, whose multiply is exact and left out
+template <int ACT, bool HAS_C, bool ALPHA1>
+__device__ __forceinline__ void epi_direct_bf16(const Epilogue &e, const DirectUniforms &u, const v16f (&acc)[4][4],
+                                                int mr0, int nc0, uint8_t *lds) {
+#pragma clang fp contract(off)
+    const int lane = lane_here();
+    // 32-bit offsets: the launcher keeps M * ldy * 2 below 2^31
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(e.y, 0, (int)(e.M * e.ldy * 2), 0x00020000);
+    const float a_s = u.a_s, s_uni = u.s_uni, c_uni = u.c_uni;
+    const bool pc = u.pc, c_vec = u.c_vec;
+    const float alpha = e.alpha, beta = e.beta;
+    const bool upper = lane >= 32;
+    const int M = (int)e.M, N = (int)e.N;
+    const uint32_t ldy2 = (uint32_t)e.ldy * 2u;
+    auto val = [&](float a, float s, float c) {
+        float v = a * s;
+        if constexpr (!ALPHA1) v *= alpha;
+        if constexpr (HAS_C) v += c;
+        return apply_act(v, ACT);
+    };
+    // column j*32 + 8g + 4*(lane/32) + q's scale and beta * C; per-channel
+    // scales and a C over N come from the copies that the tile's last step
+    // loaded into LDS (waited for by the caller)
+    // (read unconditionally, all reads issued before any use; the choices
+    // are selects, not branches)
+    auto coef = [&](int j, f4 (&sc)[4], f4 (&cb)[4]) {
+        f4 bs[4], cv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int col = j * 32 + 8 * g + 4 * upper;  // within the wavefront's 128 columns
+            bs[g] = *reinterpret_cast<const f4 *>(lds + EPD_SCALE + col * 4);
+            if constexpr (HAS_C) cv[g] = *reinterpret_cast<const f4 *>(lds + EPD_C + col * 4);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sc[g][q] = pc ? a_s * bs[g][q] : s_uni;
+                if constexpr (HAS_C) {
+                    const float c = c_vec ? cv[g][q] : c_uni;
+                    cb[g][q] = beta == 1.0f ? c : beta * c;
+                }
+            }
+    };
+    // Passes of 32 rows x 64 columns, blocks (i, 2jp) and (i, 2jp + 1),
+    // software-pipelined: a pass's values are computed while the previous
+    // pass's read-back is in flight, then that read-back is stored, this
+    // pass written and read back (LDS runs a wavefront's operations in
+    // order, so the writes follow the previous reads).
+    u4 rb[4];
+    int pm = 0, pn = 0;  // the previous pass's first row and column
+    auto store_prev = [&]() {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int m = pm + rr * 8 + (lane >> 3), n = pn + (lane & 7) * 8;
+            const uint32_t off = m < M && n < N ? (uint32_t)m * ldy2 + (uint32_t)n * 2u : OOB;
+            __builtin_amdgcn_raw_buffer_store_b128(rb[rr], ry, off, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int jp = 0; jp < 2; ++jp) {
+        f4 sc[2][4], cb[2][4];
+        coef(2 * jp, sc[0], cb[0]);
+        coef(2 * jp + 1, sc[1], cb[1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u4 pk[2][2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t px[2], py[2];
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        // x: column group g = 2h, y: g = 2h + 1; values q = 2k, 2k + 1
+                        const v16f &a = acc[i][2 * jp + jj];
+                        const f4 &sx = sc[jj][2 * h], &sy = sc[jj][2 * h + 1];
+                        const f4 &cx = cb[jj][2 * h], &cy = cb[jj][2 * h + 1];
+                        const f2 vx = {val(a[8 * h + 2 * k], sx[2 * k], cx[2 * k]),
+                                       val(a[8 * h + 2 * k + 1], sx[2 * k + 1], cx[2 * k + 1])};
+                        const f2 vy = {val(a[8 * h + 4 + 2 * k], sy[2 * k], cy[2 * k]),
+                                       val(a[8 * h + 4 + 2 * k + 1], sy[2 * k + 1], cy[2 * k + 1])};
+                        const uint32_t bx = __builtin_bit_cast(uint32_t, __builtin_convertvector(vx, bf2));
+                        const uint32_t by = __builtin_bit_cast(uint32_t, __builtin_convertvector(vy, bf2));
+                        const auto sw = __builtin_amdgcn_permlane32_swap(bx, by, false, false);
+                        px[k] = sw[0];
+                        py[k] = sw[1];
+                    }
+                    pk[jj][h] = u4{px[0], px[1], py[0], py[1]};
+                }
+            if (jp > 0 || i > 0) store_prev();
+            // row lane % 32, columns jj*32 + 16h + 8*(lane/32) .. + 7 of the pass
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<u4 *>(lds + (lane & 31) * EPD_PITCH + (jj * 32 + 16 * h + 8 * upper) * 2) =
+                        pk[jj][h];
+            // back as whole rows: 8 lanes per 128-byte row, 8 rows per store
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                rb[rr] = *reinterpret_cast<const u4 *>(lds + (rr * 8 + (lane >> 3)) * EPD_PITCH + (lane & 7) * 16);
+            pm = mr0 + i * 32;
+            pn = nc0 + jp * 64;
+        }
+    }
+    store_prev();
+}
+
 // Scheduling pattern for one step of the native FP8 loop: the NL
 // global->LDS loads first (the LDS reads may not pass them: the compiler
 // cannot tell the loads' LDS writes from the reads' addresses), then NM
@@ -280,25 +450,33 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint8_t *ld
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, off, 0, 0, 0);
 }
 
-template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV, bool PP>
+template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV, bool PP, bool DIRECT = false>
 __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_gemm_mfma(GemmArgs g) {
     using T = Tile<WAVES_M, WAVES_N, WM, WN>;
     constexpr int NSTAGE = T::NST;
+    static_assert(!DIRECT || (T::ONE_PER_SIMD && !CONV && !PP), "the persistent direct-store loop is the one-wavefront-per-SIMD GEMM's");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
     // ---- tile selection -------------------------------------------------
+    // Workgroup id -> tile: ids regrouped so that each XCD (id % 8) owns a
+    // contiguous range of tiles, walked in groups of GROUP_M tile-rows.  The
+    // persistent kernel walks ids blockIdx.x, + gridDim.x, ... (gridDim.x a
+    // multiple of 8 whenever it is below the tile count, so every id of one
+    // workgroup stays on its XCD's range).
     const int ntiles = g.tiles_m * g.tiles_n;
-    int t = blockIdx.x;
-    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
-    const int per_group = GROUP_M * g.tiles_n;
-    const int group = t / per_group;
-    const int first_m = group * GROUP_M;
-    const int gsize = min(g.tiles_m - first_m, GROUP_M);
-    const int tm = first_m + (t % per_group) % gsize;
-    const int tn = (t % per_group) / gsize;
-    const int64_t m0 = (int64_t)tm * T::BM, n0 = (int64_t)tn * T::BN;
+    auto tile_origin = [&](int t, int64_t &om0, int64_t &on0) {
+        if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+        const int per_group = GROUP_M * g.tiles_n;
+        const int group = t / per_group;
+        const int first_m = group * GROUP_M;
+        const int gsize = min(g.tiles_m - first_m, GROUP_M);
+        om0 = (int64_t)(first_m + (t % per_group) % gsize) * T::BM;
+        on0 = (int64_t)((t % per_group) / gsize) * T::BN;
+    };
+    int64_t m0, n0;
+    tile_origin(blockIdx.x, m0, n0);
 
     // ---- global -> LDS block assignment ----------------------------------
     // A: 1 KB block b holds rows (1024/BK)*b ..; B: block b holds panel b/CPR,
@@ -315,6 +493,13 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
     // CONV: where the block's chunk of the next step to issue lies in (kh, kw, c)
     int a_c[CONV ? T::A_BLK : 1], a_kw[CONV ? T::A_BLK : 1], a_kh[CONV ? T::A_BLK : 1];
+    // the load offsets of the tile at (m0, n0); valid = false: every load
+    // out of range (a persistent workgroup past its last tile)
+    // (ln, wv: the lane and wavefront index; the persistent kernel passes a
+    // lane index computed on the spot, so that nothing per lane is held
+    // through its main loop for this)
+    auto setup_offsets = [&](int64_t m0, int64_t n0, bool valid, int ln, int wv) {
+        const int lane = ln, wave = wv;
 #pragma unroll
     for (int i = 0; i < T::A_BLK; ++i) {
         const int r = (wave * T::A_BLK + i) * (1024 / BK) + lane / CPR;
@@ -340,16 +525,20 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             }
             a_c[i] = cc; a_kw[i] = kw; a_kh[i] = kh;
         } else {
-            a_off[i] = (m0 + r < g.M) ? (uint32_t)((m0 + r) * g.lda + c * 16) : OOB;
-            a_klim[i] = (m0 + r < g.M) ? (uint32_t)g.K : 0u;
+            // 32-bit: the host keeps (M - 1) * lda + K below 2^31
+            const bool in = (int)m0 + r < (int)g.M;
+            a_off[i] = valid && in ? ((uint32_t)m0 + (uint32_t)r) * (uint32_t)g.lda + (uint32_t)(c * 16) : OOB;
+            a_klim[i] = in ? (uint32_t)g.K : 0u;
         }
     }
 #pragma unroll
     for (int i = 0; i < T::B_BLK; ++i) {
         const int b = wave * T::B_BLK + i;
         const int64_t panel = (n0 >> 6) + b / CPR;
-        b_off[i] = panel < g.npanels ? (uint32_t)((panel * g.KC + b % CPR) * 1024 + lane * 16) : OOB;
+        b_off[i] = valid && panel < g.npanels ? (uint32_t)((panel * g.KC + b % CPR) * 1024 + lane * 16) : OOB;
     }
+    };
+    setup_offsets(m0, n0, true, lane, wave);
     auto issue_tile = [&](int kt, int stage) {
         uint8_t *sa = smem + stage * T::STAGE;
         const uint32_t kbyte = (uint32_t)kt * BK;
@@ -552,8 +741,18 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // 4), so they lie 32*BK bytes apart; B's 32-column block j of this
         // wavefront's 128 columns sits (j/2) panels and (j%2)*32 columns past
         // block 0.
-        const int ra0 = a_lds_off(a_r0, kgrp), ra1 = a_lds_off(a_r0, kgrp + 1);
-        const int rb = T::A_BYTES + b_off_lds[0] + kgrp * 1024;
+        int ra0 = a_lds_off(a_r0, kgrp), ra1 = a_lds_off(a_r0, kgrp + 1);
+        int rb = T::A_BYTES + b_off_lds[0] + kgrp * 1024;
+        // the same bases from a lane index computed on the spot (the
+        // persistent kernel recomputes them after each tile's epilogue
+        // instead of holding them through it)
+        auto frag_bases = [&](int ln, int wv) {
+            const int kg = (ln >> 5) * 2, r0 = (wv / WAVES_N) * WM * 32 + (ln & 31);
+            const int col = (wv % WAVES_N) * WN * 32;
+            ra0 = a_lds_off(r0, kg);
+            ra1 = a_lds_off(r0, kg + 1);
+            rb = T::A_BYTES + (col >> 6) * (CPR * 1024) + ((col & 63) + (ln & 31)) * 16 + kg * 1024;
+        };
         auto frag = [&](u4 (&f)[NF][2], int q) -> u4 & {
             const int blk = q >> 1;
             return f[blk == 0 ? 0 : blk <= 4 ? WM + blk - 1 : blk - 4][q & 1];
@@ -567,7 +766,17 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             frag(f, q) = *reinterpret_cast<const u4 *>(p);
         };
         // load l (A blocks, then B) of step lt into the stage at `lst`
+        // DIRECT (persistent walk): the workgroup's next tile, whose first
+        // NSTAGE-1 steps the last steps of the current tile load
+        int tb = blockIdx.x;
+        int64_t nm0 = 0, nn0 = 0;
+        bool has_next = false;
         auto load = [&](uint8_t *lst, int lt, int l, bool checked) {
+            // DIRECT: steps past the tile's end are the next tile's first
+            // ones, and by then a_off / b_off are the next tile's (switched
+            // before the first step that loads them)
+            if constexpr (DIRECT)
+                if (checked && lt >= g.nk) lt -= g.nk;
             const uint32_t kbyte = (uint32_t)lt * BK;
             if (l < T::A_BLK) {
                 // rows past M carry OOB, and OOB + kbyte stays out of range;
@@ -595,40 +804,90 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             o[x] = (sub & 1) ? e4m3x8_to_bf16(w.z, w.w) : e4m3x8_to_bf16(w.x, w.y);
         };
         // rso: stage offset of step kt+1 (read), lso: of step kt+NSTAGE-1 (loaded)
-        auto step = [&](u4 (&fc)[NF][2], u4 (&fn)[NF][2], int kt, int rso, int lso, bool checked) {
+        // DIRECT: the tile's last step also loads, ahead of its ring loads,
+        // this wavefront's 128 columns of per-channel scales and of a C over
+        // N into its part of the free ring stage (that of the step itself:
+        // the stage before rso), for the epilogue, which waits for them
+        // with vmcnt(LOADS).  Lanes 0-31 load 16 bytes each; the rest, and
+        // everything when there is nothing to load, read out of range.
+        const __amdgpu_buffer_rsrc_t sc_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)g.e.b_scale, 0, g.e.b_scale && g.e.b_per_channel ? (int)(g.e.N * 4) : 0, 0x00020000);
+        const bool c_over_n = g.e.c && !(g.e.c_ndim == 0 || (g.e.c_ndim == 1 && g.e.c0 == 1) ||
+                                         (g.e.c_ndim == 2 && g.e.c1 == 1));
+        const __amdgpu_buffer_rsrc_t c_rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void *)g.e.c, 0, c_over_n ? (int)(g.e.N * 4) : 0, 0x00020000);
+        auto load_coef = [&](int rso_now) {
+            if constexpr (DIRECT) {
+                uint8_t *dst = smem + (rso_now >= T::STAGE ? rso_now - T::STAGE : (NSTAGE - 1) * T::STAGE) +
+                               wave_u * EPD_BYTES;
+                const int ln = lane_here();
+                const int col = (int)n0 + (wave_u % WAVES_N) * WN * 32 + 4 * ln;
+                const uint32_t off = ln < 32 && col < (int)g.N ? (uint32_t)col * 4u : OOB;
+                lds_load16(sc_rsrc, dst + EPD_SCALE, off);
+                lds_load16(c_rsrc, dst + EPD_C, off);
+            }
+        };
+        // first (DIRECT): the tile's first step, whose MFMAs start from zero
+        // instead of the accumulators
+        const v16f vzero = {};
+        // last (DIRECT): a tile's last step, which reads no fragments of the
+        // next step (they are read after the tile's epilogue, so that they
+        // are not held through it)
+        auto step = [&](u4 (&fc)[NF][2], u4 (&fn)[NF][2], int kt, int rso, int lso, bool checked,
+                        auto first, auto last) {
+            constexpr bool FIRST = decltype(first)::value, LAST = decltype(last)::value;
             const uint8_t *rst = stage0 + rso;
             uint8_t *lst = smem + lso;
             const int lt = kt + NSTAGE - 1;
+            // DIRECT: the fragment bases are recomputed at every step, so
+            // that no per-lane value is held through the tile epilogues
+            if constexpr (DIRECT) frag_bases(lane_here(), wave_u);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (EXACT) {
                 // 4 substeps of 16 bf16 MFMAs; each substep widens the next
                 // one's fragments (two conversions per MFMA), the last one
                 // the next step's first substep
-                auto mma = [&](const bf16x8 (&o)[NF], int b) {
+                // DIRECT: operands swapped (B block first), so that a lane's
+                // accumulators hold one output row (epi_direct_bf16)
+                auto mma = [&](const bf16x8 (&o)[NF], int b, auto zero_c) {
                     const int i = b / WN, j = b % WN;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o[i], o[WM + j], acc[i][j], 0, 0, 0);
+                    const v16f &c = decltype(zero_c)::value ? vzero : acc[i][j];
+                    if constexpr (DIRECT)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o[WM + j], o[i], c, 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o[i], o[WM + j], c, 0, 0, 0);
                 };
+                using Acc = std::false_type;
+                // DIRECT: a tile's first step widens its own first substep
+                // (nothing converted is held through the loop's back edge)
+                if constexpr (DIRECT && FIRST) {
+                    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fc landed
+#pragma unroll
+                    for (int x = 0; x < NF; ++x) conv(cv0, fc, 0, x);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 // substep 0: the barrier after 2 MFMAs, then 14 reads
 #pragma unroll
                 for (int b = 0; b < 16; ++b) {
-                    mma(cv0, b);
+                    mma(cv0, b, std::integral_constant<bool, FIRST>{});
                     if ((b & 1) == 0) conv(cv1, fc, 1, b >> 1);
-                    if (b >= 2) read(fn, rst, b - 2);
+                    if (!LAST && b >= 2) read(fn, rst, b - 2);
                     __builtin_amdgcn_sched_barrier(0);
                     if (b == 1) sync_step();
                 }
                 // substep 1: the last 2 reads, the 8 loads
 #pragma unroll
                 for (int b = 0; b < 16; ++b) {
-                    mma(cv1, b);
+                    mma(cv1, b, Acc{});
                     if ((b & 1) == 0) conv(cv0, fc, 2, b >> 1);
-                    if (b < 2) read(fn, rst, 14 + b);
+                    if (!LAST && b < 2) read(fn, rst, 14 + b);
+                    if (LAST && b == 2) load_coef(rso);
                     if (b >= 2 && b < 2 + T::LOADS) load(lst, lt, b - 2, checked);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int b = 0; b < 16; ++b) {
-                    mma(cv0, b);
+                    mma(cv0, b, Acc{});
                     if ((b & 1) == 0) conv(cv1, fc, 3, b >> 1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -636,8 +895,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int b = 0; b < 16; ++b) {
-                    mma(cv1, b);
-                    if ((b & 1) == 0) conv(cv0, fn, 0, b >> 1);
+                    mma(cv1, b, Acc{});
+                    if (!LAST && (b & 1) == 0) conv(cv0, fn, 0, b >> 1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
@@ -645,8 +904,13 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 // barrier, the 8 loads on the last 6
                 auto mma = [&](int b) {
                     const int i = b / WN, j = b % WN;
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        join(fc[i][0], fc[i][1]), join(fc[WM + j][0], fc[WM + j][1]), acc[i][j], 0, 0, 0, 0, 0, 0);
+                    const v16f &c = FIRST ? vzero : acc[i][j];
+                    if constexpr (DIRECT)  // operands swapped, as in the exact loop
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            join(fc[WM + j][0], fc[WM + j][1]), join(fc[i][0], fc[i][1]), c, 0, 0, 0, 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            join(fc[i][0], fc[i][1]), join(fc[WM + j][0], fc[WM + j][1]), c, 0, 0, 0, 0, 0, 0);
                 };
                 __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fc landed
                 mma(0);
@@ -657,9 +921,12 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 for (int b = 2; b < 16; ++b) {
                     mma(b);
                     if (b < 10) {
-                        read(fn, rst, 2 * (b - 2));
-                        read(fn, rst, 2 * (b - 2) + 1);
+                        if (!LAST) {
+                            read(fn, rst, 2 * (b - 2));
+                            read(fn, rst, 2 * (b - 2) + 1);
+                        }
                     } else {
+                        if (LAST && b == 10) load_coef(rso);
 #pragma unroll
                         for (int n = (T::LOADS - l + 15 - b) / (16 - b); n > 0; --n, ++l) load(lst, lt, l, checked);
                     }
@@ -669,7 +936,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         };
 #pragma unroll
         for (int q = 0; q < 16; ++q) read(f0, stage_a(0), q);
-        if constexpr (EXACT) {
+        if constexpr (EXACT && !DIRECT) {  // DIRECT: the first step converts
             __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
 #pragma unroll
             for (int x = 0; x < NF; ++x) conv(cv0, f0, 0, x);
@@ -682,13 +949,93 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // steps whose loads (of step kt+NSTAGE-1) lie inside K need no k test
         const int nfull = (int)(g.K / BK);
         const int l1 = (nfull - (NSTAGE - 1) > 0 ? nfull - (NSTAGE - 1) : 0) & ~1;
-        for (int kt = 0; kt < l1; kt += 2) {
-            step(f0, f1, kt, rso, lso, false); adv();
-            step(f1, f0, kt + 1, rso, lso, false); adv();
-        }
-        for (int kt = l1; kt < g.nk; kt += 2) {
-            step(f0, f1, kt, rso, lso, true); adv();
-            step(f1, f0, kt + 1, rso, lso, true); adv();
+        using No = std::false_type;
+        if constexpr (DIRECT) {
+            // Persistent walk over tiles tb = blockIdx.x, + gridDim.x, ...:
+            // the ring runs on across tile boundaries (the last steps of a
+            // tile load the next tile's first ones, and its last step reads
+            // the next tile's first fragments), and each tile's epilogue
+            // stores straight from the accumulators, so nothing of the LDS
+            // is needed between tiles and the next tile's loads are in
+            // flight meanwhile.  The first step of a tile starts its MFMAs
+            // from zero.  nk is even, so every tile starts on f0.
+            auto find_next = [&]() {
+                has_next = tb + (int)gridDim.x < ntiles;
+                if (has_next) tile_origin(tb + (int)gridDim.x, nm0, nn0);
+            };
+            find_next();
+            const DirectUniforms du = direct_uniforms(g.e);
+            // wavefront-uniform (scalar) row and column offsets of this wavefront
+            const int mr0 = (wave_u / WAVES_N) * WM * 32, nc0 = (wave_u % WAVES_N) * WN * 32;
+            using Yes = std::true_type;
+            static_assert(NSTAGE == 5, "the offset switch sits four steps before a tile's end");
+            static_assert(T::NW * EPD_BYTES <= T::STAGE, "the epilogue staging fits one ring stage");
+            static_assert(T::LOADS <= 63, "vmcnt field");
+            // from step nk - 4 on, the steps load the next tile's first ones
+            auto switch_offsets = [&]() { setup_offsets(nm0, nn0, has_next, lane_here(), wave_u); };
+            for (;;) {
+                // nk >= 4 (the launcher's condition) and even: a first pair,
+                // the middle pairs, the offset switch, the last two pairs
+                if (g.nk == 4) switch_offsets();
+                step(f0, f1, 0, rso, lso, true, Yes{}, No{}); adv();
+                step(f1, f0, 1, rso, lso, true, No{}, No{}); adv();
+                if (g.nk > 4) {
+                    for (int kt = 2; kt < l1; kt += 2) {
+                        step(f0, f1, kt, rso, lso, false, No{}, No{}); adv();
+                        step(f1, f0, kt + 1, rso, lso, false, No{}, No{}); adv();
+                    }
+                    for (int kt = l1 > 2 ? l1 : 2; kt < g.nk - 4; kt += 2) {
+                        step(f0, f1, kt, rso, lso, true, No{}, No{}); adv();
+                        step(f1, f0, kt + 1, rso, lso, true, No{}, No{}); adv();
+                    }
+                    switch_offsets();
+                    step(f0, f1, g.nk - 4, rso, lso, true, No{}, No{}); adv();
+                    step(f1, f0, g.nk - 3, rso, lso, true, No{}, No{}); adv();
+                }
+                step(f0, f1, g.nk - 2, rso, lso, true, No{}, No{}); adv();
+                step(f1, f0, g.nk - 1, rso, lso, true, No{}, Yes{}); adv();
+                __builtin_amdgcn_sched_barrier(0);
+                const Epilogue &e = g.e;
+                // the ring stage of this tile's last step: its fragments were
+                // read in the step before, every wavefront is past that
+                // step's barrier, and the next loads into it follow the next
+                // step's barrier
+                uint8_t *est = smem + (rso >= 2 * T::STAGE ? rso - 2 * T::STAGE : rso + (NSTAGE - 2) * T::STAGE) +
+                               wave_u * EPD_BYTES;
+                // the coefficient loads landed: only the last step's ring
+                // loads, issued after them, may still be in flight
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(T::LOADS) : "memory");
+                const int mt = (int)m0 + mr0, nt = (int)n0 + nc0;
+                if (e.alpha == 1.0f) {
+                    if (e.c) epi_direct_bf16<ACT_NONE, true, true>(e, du, acc, mt, nt, est);
+                    else epi_direct_bf16<ACT_NONE, false, true>(e, du, acc, mt, nt, est);
+                } else {
+                    if (e.c) epi_direct_bf16<ACT_NONE, true, false>(e, du, acc, mt, nt, est);
+                    else epi_direct_bf16<ACT_NONE, false, false>(e, du, acc, mt, nt, est);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (!has_next) break;
+                tb += (int)gridDim.x;
+                m0 = nm0;
+                n0 = nn0;
+                find_next();
+                // the next tile's first fragments: step 0's stage, the one
+                // before rso (it landed by the last step's barrier, and no
+                // load targets it before the next step's barrier)
+                frag_bases(lane_here(), wave_u);  // for the reads below
+                const uint8_t *st0 = stage0 + (rso == 0 ? (NSTAGE - 1) * T::STAGE : rso - T::STAGE);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) read(f0, st0, q);
+            }
+        } else {
+            for (int kt = 0; kt < l1; kt += 2) {
+                step(f0, f1, kt, rso, lso, false, No{}, No{}); adv();
+                step(f1, f0, kt + 1, rso, lso, false, No{}, No{}); adv();
+            }
+            for (int kt = l1; kt < g.nk; kt += 2) {
+                step(f0, f1, kt, rso, lso, true, No{}, No{}); adv();
+                step(f1, f0, kt + 1, rso, lso, true, No{}, No{}); adv();
+            }
         }
     } else if constexpr (EXACT) {
         // Each lane's 64-k fragment is two 16-byte chunks (lo: chunk kgrp,
@@ -768,6 +1115,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tail's loads land before the LDS is reused
+    if constexpr (DIRECT) return;  // every tile's epilogue ran in the persistent loop
     __syncthreads();
 
     // ---- epilogue --------------------------------------------------------
@@ -1003,9 +1351,22 @@ using Small = Tile<2, 2, 2, 2>;
 // a five-stage ring (the k_gemm_mfma loop for Tile::ONE_PER_SIMD).
 using Wide = Tile<2, 2, 4, 4>;
 
-template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false>
+// compute units of the current device (the persistent grid's size), cached per device
+int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false, bool DIRECT = false>
 hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
-    auto *fn = k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP>;
+    auto *fn = k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT>;
     static std::atomic<uint64_t> lds_set{0};
     if (hipError_t err = ensure_dynamic_lds(reinterpret_cast<const void *>(fn), Cfg::LDS_BYTES, lds_set);
         err != hipSuccess)
@@ -1020,9 +1381,12 @@ hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
     // launched by name, as every other kernel here: a launch through the
     // pointer variable returned success without running the kernel when the
     // host pass was built with -fsanitize=address,undefined
-    hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP>),
-                       dim3(g.tiles_m * g.tiles_n, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES,
-                       s, g);
+    // the persistent kernel: one workgroup per CU (its LDS use allows no
+    // more), each walking tiles blockIdx.x + k * gridDim.x
+    int grid = g.tiles_m * g.tiles_n;
+    if constexpr (DIRECT) grid = grid < device_cus() ? grid : device_cus();
+    hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT>),
+                       dim3(grid, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES, s, g);
     return hipGetLastError();
 }
 
@@ -1041,10 +1405,29 @@ static_assert(!LCML_GEMM_PINGPONG || (WAVES_M == 2 && WAVES_M * WAVES_N == 8), "
 // faster: a bf16 output (with fp32 the epilogue of its 128x128 wavefront
 // tiles costs more than the main loop gains) on a grid of more than one
 // tile column.
+#ifndef LCML_GEMM_DIRECT
+#define LCML_GEMM_DIRECT 1
+#endif
+// The persistent direct-store variant of the one-wavefront-per-SIMD layout
+// takes the outputs its epilogue covers: N and the row pitch multiples of 8,
+// a 16-byte aligned y whose M rows of pitch stay below 2^31 bytes, C absent
+// or row-invariant, no activation (the others keep the staged epilogue);
+// and K > 128, so that a tile has at least four 64-k steps.
+bool direct_epilogue_ok(const Epilogue &e) {
+    const bool c_ok = !e.c || e.c_ndim == 0 || (e.c_ndim == 1 && (e.c0 == 1 || e.c0 == e.N)) ||
+                      (e.c_ndim == 2 && e.c0 == 1);
+    return LCML_GEMM_DIRECT && e.y_bf16 && c_ok && e.act == ACT_NONE && e.N % 8 == 0 &&
+           e.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(e.y) & 15) == 0 &&
+           e.M * e.ldy * 2 < ((int64_t)1 << 31);
+}
+
 template <bool EXACT, bool CONV>
 hipError_t launch(GemmArgs &g, hipStream_t s) {
     if constexpr (!CONV)
-        if (g.e.y_bf16 && g.N > Wide::BN) return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false>(g, s);
+        if (g.e.y_bf16 && g.N > Wide::BN) {
+            if (direct_epilogue_ok(g.e) && g.K > kPackK) return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false, false, true>(g, s);
+            return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false>(g, s);
+        }
     return launch_cfg<Shipped, WAVES_M, WAVES_N, WM, WN, EXACT, CONV, EXACT && (bool)LCML_GEMM_PINGPONG>(g, s);
 }
 

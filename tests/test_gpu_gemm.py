@@ -226,6 +226,50 @@ def test_mfma_epilogue_huge_row_pitch(dev, kernel, out_dtype, ldy, M):
     assert int((buf != fill).sum().item()) == 0
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "mfma_fp8"])
+@pytest.mark.parametrize("M,N,K", [(4100, 4104, 1008), (4352, 4352, 160), (300, 1000, 320), (8200, 2056, 2048)])
+@pytest.mark.parametrize("epi", ["plain", "bias_relu", "scalar_c_alpha"])
+def test_mfma_persistent_direct_store(dev, kernel, M, N, K, epi):
+    """bf16 outputs with N and the row pitch multiples of 8 take the
+    persistent one-wavefront-per-SIMD kernel, whose workgroups walk several
+    tiles (more tiles than CUs here: 289, 289 and 297 tiles; a grid of 12
+    at 300 x 1000), with ragged last tile rows and columns, K of 4, 5 and 16
+    steps, and an epilogue that stores straight from the accumulators.  Its
+    output must be, bit for bit, the bf16 rounding of the same kernel
+    family's fp32 output (the 2x4 layout with the staged epilogue), write
+    nothing outside its [M, N] view of a pitched buffer, and match the
+    oracle on sampled rows."""
+    per_channel = epi != "scalar_c_alpha"
+    c = make_case(M, N, K, seed=M + N + K, per_channel=per_channel, dev=dev)
+    if epi == "plain":
+        kw, bias = dict(), None
+    elif epi == "bias_relu":
+        bias = make_bias("N", M, N, seed=17)
+        kw = dict(bias=bias, act=capi.ACT_RELU)
+    else:
+        bias = make_bias("1", M, N, seed=19)
+        kw = dict(bias=bias, alpha=0.75, beta=-1.25)
+    y32 = run(c, KERNELS[kernel], dev=dev, **kw)
+    ld = N + 24
+    fill = -12288.0
+    buf = torch.full((M, ld), fill, dtype=torch.bfloat16, device=dev)
+    view = buf[:, :N]
+    d_bias = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias, np.float32)).to(dev)
+    capi.gemm(c.d_qa, c.d_sa, c.d_bp, c.d_sb, c.N, c.K, c=d_bias, alpha=kw.get("alpha", 1.0),
+              beta=kw.get("beta", 1.0), act=kw.get("act", capi.ACT_NONE), out=view, kernel=KERNELS[kernel])
+    torch.cuda.synchronize()
+    assert torch.equal(view.view(torch.int16), y32.to(torch.bfloat16).view(torch.int16))
+    assert bool((buf[:, N:] == fill).all())
+    if kernel == "mfma":
+        rows = np.unique(np.array([0, 1, 255, 256, M // 2, M - 2, M - 1]))
+        sub = c.__class__()
+        sub.__dict__.update(c.__dict__)
+        sub.qa = c.qa[rows]
+        ref, bound = reference(sub, bias=None if bias is None else (bias if bias.ndim < 2 else bias[rows]),
+                               alpha=kw.get("alpha", 1.0), beta=kw.get("beta", 1.0), act=kw.get("act", capi.ACT_NONE))
+        assert_close(y32[torch.from_numpy(rows).to(dev)].cpu().numpy(), ref, bound, act=kw.get("act", capi.ACT_NONE))
+
+
 def test_kernels_agree_small_m(dev):
     """All three kernels on one decode-shaped case agree within the bound."""
     c = make_case(16, 2048, 4096, seed=21, dev=dev)
