@@ -255,7 +255,7 @@ def main() -> int:
     # graph like the GEMM launches; best over a few grid sizes
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     floor = {}
-    for wgs in (172, 256, 512, 1024, 2048):
+    for wgs in (172, 256, 512, 768, 1024, 2048):
         gf = capture(lambda i, wgs=wgs: capi.stream_read(packed[i % N_WEIGHT_COPIES], sink, wgs), 3 * args.steps)
         gf.replay()
         floor[str(wgs)] = round(1e3 * timed(gf.replay) / (3 * args.steps), 2)

@@ -389,8 +389,10 @@ LCML_API int lcml_fp8_binary(int op, int dtype, const void *a, const int64_t *a_
 /*
  * Measurement aid, no counterpart in the reference: reads `bytes` bytes
  * (a multiple of 16) at 16-byte aligned device pointer p with `workgroups`
- * workgroups of 256 threads and does nothing else (`sink`: one device word,
- * written only when a fold of the data equals a fixed constant).  Its time
+ * workgroups of 512 threads, each streaming one contiguous, equal share
+ * (below 2 GiB) with non-temporal loads, and does nothing else (`sink`: one
+ * device word, written only when a fold of the data equals a fixed
+ * constant).  Its time
  * over a buffer is the HBM read floor that the bandwidth-bound small-M GEMM
  * (which reads the same weight bytes once) is compared with.
  */

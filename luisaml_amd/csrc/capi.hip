@@ -582,6 +582,9 @@ int lcml_fp8_stream_read(const void *p, int64_t bytes, int workgroups, uint32_t 
                     workgroups);
     if (bytes == 0) return LCML_OK;
     if (!p || !sink || !aligned(p, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: p must be 16-byte aligned, sink set", fn);
+    if ((bytes / 16 + workgroups - 1) / workgroups >= ((int64_t)1 << 27))
+        return fail(LCML_ERR_UNSUPPORTED, "%s: a workgroup's share of %lld bytes over %d workgroups exceeds 2 GiB", fn,
+                    (long long)bytes, workgroups);
     return hip_status(lcml::launch_stream_read(p, bytes, workgroups, sink, (hipStream_t)stream), fn);
 }
 

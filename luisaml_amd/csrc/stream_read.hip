@@ -1,31 +1,41 @@
 // stream_read.hip -- a read-only streaming kernel: the HBM read floor that
 // the bandwidth-bound small-M GEMM is measured against (the same bytes with
-// no arithmetic and no output stream).  Each thread keeps four independent
-// 16-byte loads in flight per iteration of a grid-stride loop and folds them
-// into one word, which is stored only when it equals a fixed constant: the
-// loads cannot be removed, and the kernel writes (almost) nothing.
+// no arithmetic and no output stream).  Each workgroup streams one
+// contiguous, equal share of the bytes with non-temporal 16-byte buffer
+// loads, two per thread in flight per iteration (the shape that read the
+// packed 4096x11008 weight fastest in a sweep of grid sizes, threads,
+// loads in flight and grid-stride against contiguous shares), and folds
+// them into one word, which is stored only when it equals a fixed constant:
+// the loads cannot be removed, and the kernel writes (almost) nothing.
 #include "lcml_internal.hpp"
 
 namespace lcml {
 namespace {
 
-constexpr int kThreads = 256, kUnroll = 4;
+constexpr int kThreads = 512, kUnroll = 2;
+constexpr int kNT = 2;                  // buffer load cache policy: non-temporal
+constexpr uint32_t kOOB = 0x80000000u;  // offset past the extent: zeros, no memory access
 
-__global__ __launch_bounds__(kThreads) void k_stream_read(const uint4 *__restrict__ p, int64_t n16,
-                                                          uint32_t *sink) {
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kThreads) void k_stream_read(const uint8_t *__restrict__ p, int64_t n16,
+                                                          int64_t per_wg, uint32_t *sink) {
+    // this workgroup's share: 16-byte units [b0, b1)
+    const int64_t b0 = (int64_t)blockIdx.x * per_wg;
+    const int64_t b1 = b0 + per_wg < n16 ? b0 + per_wg : n16;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p + (b0 < n16 ? b0 : 0) * 16), 0, b1 > b0 ? (int)((b1 - b0) * 16) : 0, 0x00020000);
+    const int64_t units = b1 > b0 ? b1 - b0 : 0;
     uint32_t acc = 0;
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
-        uint4 v[kUnroll];
+    for (int64_t i = threadIdx.x; i < units; i += (int64_t)kThreads * kUnroll) {
+        u4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = p[i + u * stride];
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t j = i + (int64_t)u * kThreads;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, j < units ? (int)(j * 16) : (int)kOOB, 0, kNT);
+        }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; i < n16; i += stride) {
-        const uint4 v = p[i];
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9e3779b9u) sink[0] = acc;
 }
@@ -33,8 +43,10 @@ __global__ __launch_bounds__(kThreads) void k_stream_read(const uint4 *__restric
 }  // namespace
 
 hipError_t launch_stream_read(const void *p, int64_t bytes, int workgroups, uint32_t *sink, hipStream_t s) {
-    hipLaunchKernelGGL(k_stream_read, dim3(workgroups), dim3(kThreads), 0, s, static_cast<const uint4 *>(p),
-                       bytes / 16, sink);
+    const int64_t n16 = bytes / 16;
+    const int64_t per_wg = (n16 + workgroups - 1) / workgroups;  // < 2^27: each share's offsets fit 31 bits
+    hipLaunchKernelGGL(k_stream_read, dim3(workgroups), dim3(kThreads), 0, s, static_cast<const uint8_t *>(p), n16,
+                       per_wg, sink);
     return hipGetLastError();
 }
 
