@@ -72,19 +72,26 @@ def make_c(kind, M, N, seed):
     return np.array(np.random.default_rng(seed).standard_normal(shape) * 0.05, dtype=np.float32)
 
 
+SPARE_ROWS = 256  # buffer rows past M: the stores of a tile's rows past M must be dropped
+
+
 def out_buffer(layout, M, N, pad, dtype, dev):
+    """The output view in a larger buffer filled with FILL (256 spare rows
+    past M in every layout), and the mask of the elements outside the view."""
     if layout == "dense":
-        buf = torch.full((M, N), FILL, dtype=dtype, device=dev)
-        return buf, buf, None
-    if layout == "pitch":
-        buf = torch.full((M, N + pad), FILL, dtype=dtype, device=dev)
+        buf = torch.full((M + SPARE_ROWS, N), FILL, dtype=dtype, device=dev)
         mask = torch.ones_like(buf, dtype=torch.bool)
-        mask[:, :N] = False
-        return buf, buf[:, :N], mask
-    buf = torch.full((M * N + 1,), FILL, dtype=dtype, device=dev)
+        mask[:M] = False
+        return buf, buf[:M], mask
+    if layout == "pitch":
+        buf = torch.full((M + SPARE_ROWS, N + pad), FILL, dtype=dtype, device=dev)
+        mask = torch.ones_like(buf, dtype=torch.bool)
+        mask[:M, :N] = False
+        return buf, buf[:M, :N], mask
+    buf = torch.full(((M + SPARE_ROWS) * N + 1,), FILL, dtype=dtype, device=dev)
     mask = torch.ones_like(buf, dtype=torch.bool)
-    mask[1:] = False
-    return buf, buf[1:].view(M, N), mask
+    mask[1:1 + M * N] = False
+    return buf, buf[1:1 + M * N].view(M, N), mask
 
 
 def check(y, ref, bound, p):

@@ -1,8 +1,9 @@
 """lcml_fp8_gemm_dynamic_noalloc against lcml_fp8_gemm_dynamic through the C
 ABI: bit-identical outputs and scales on consecutive calls that share the
 library's scratch array (the largest accepted M*K first, then a smaller
-two-step call, then a fused small-M call), and no change in the device's
-free memory across a call."""
+two-step call, then a fused small-M call), no change in the device's free
+memory across a call, and the same bits from calls captured into a HIP
+graph and replayed."""
 import numpy as np
 import pytest
 import torch
@@ -16,14 +17,15 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
-def noalloc(x, bp, sw, N, K, c=None, act=capi.ACT_NONE, out_dtype=torch.float32, scale_out=None, out=None):
+def noalloc(x, bp, sw, N, K, c=None, act=capi.ACT_NONE, out_dtype=torch.float32, scale_out=None, out=None,
+            stream=None):
     M = x.shape[0]
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x.device)
     ydt = capi.DTYPE_BFLOAT16 if out_dtype == torch.bfloat16 else capi.DTYPE_FLOAT
     rc = capi.lib().lcml_fp8_gemm_dynamic_noalloc(M, N, K, _ptr(x), x.stride(0), _ptr(bp), _ptr(sw),
                                                   int(sw.numel() > 1), 1.0, _ptr(c), 1 if c is not None else 0,
                                                   N if c is not None else 0, 0, 1.0, act, _ptr(y), ydt, N,
-                                                  _ptr(scale_out), capi.KERNEL_AUTO, None)
+                                                  _ptr(scale_out), capi.KERNEL_AUTO, stream)
     assert rc == capi.OK, capi.last_error()
     return y
 
@@ -70,3 +72,53 @@ def test_noalloc_two_calls_in_a_row_second_smaller(dev):
     assert torch.cuda.mem_get_info()[0] == free0
     assert torch.equal(y1.view(torch.int32), refs[0].view(torch.int32))
     assert torch.equal(y2.view(torch.int32), refs[1].view(torch.int32))
+
+
+def test_noalloc_captured_in_a_graph(dev):
+    """The callers it is for: calls captured into a HIP graph (a two-step
+    call, whose quantised activations and scale live in the scratch array,
+    then a fused small-M call), replayed four times with unrelated eager
+    work between replays; every replay gives the outputs and scales of
+    lcml_fp8_gemm_dynamic bit for bit, and the replays leave the device's
+    free memory unchanged."""
+    two = case(21, 96, 2048, 704, dev)   # M*K > 16384: quantise into the scratch, then the GEMM
+    fused = case(22, 4, 1024, 320, dev)  # the fused skinny kernel
+    s_ref = [torch.empty(1, device=dev) for _ in range(2)]
+    refs = [capi.gemm_dynamic(two[0], two[1], two[2], 704, 2048, c=two[3], out_dtype=torch.bfloat16,
+                              scale_out=s_ref[0]),
+            capi.gemm_dynamic(fused[0], fused[1], fused[2], 320, 1024, c=fused[3], act=capi.ACT_GELU_ERF,
+                              scale_out=s_ref[1])]
+    ys = [torch.empty_like(refs[0]), torch.empty_like(refs[1])]
+    ss = [torch.empty(1, device=dev) for _ in range(2)]
+
+    def calls(stream):
+        noalloc(two[0], two[1], two[2], 704, 2048, c=two[3], out_dtype=torch.bfloat16, scale_out=ss[0], out=ys[0],
+                stream=stream)
+        noalloc(fused[0], fused[1], fused[2], 320, 1024, c=fused[3], act=capi.ACT_GELU_ERF, scale_out=ss[1],
+                out=ys[1], stream=stream)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls(side.cuda_stream)  # warm, outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        calls(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for r in range(4):
+        for t in ys + ss:
+            t.zero_()
+        other = capi.gemm_dynamic(two[0], two[1], two[2], 704, 2048)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys[0].view(torch.int16), refs[0].view(torch.int16)), f"replay {r}"
+        assert torch.equal(ys[1].view(torch.int32), refs[1].view(torch.int32)), f"replay {r}"
+        for i in range(2):
+            assert torch.equal(ss[i].view(torch.int32), s_ref[i].view(torch.int32)), f"replay {r} scale {i}"
+        del other
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
