@@ -214,6 +214,35 @@ LCML_API int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float 
                           void *workspace, int64_t workspace_bytes, int kernel, void *stream);
 
 /*
+ * lcml_fp8_gemm_dynamic for a chain of dynamically quantised linears (the
+ * fp32 output of one is the next one's input, as the up-projection's GELU
+ * output feeds the down-projection): the amax pass over an activation moves
+ * into the epilogue that produces it.  No counterpart in the reference
+ * (whose composition recomputes ReduceMax over each input).  Arguments as
+ * for lcml_fp8_gemm_dynamic, plus:
+ * y_amax_part (optional): receives partial maxima of y, *y_amax_npart words
+ *   (written by the call, on the host), each the fp32 bits of max |y| over a
+ *   part of y (NaN skipped), the parts covering y; y must then be fp32 and
+ *   dense (ldy == N) and the buffer hold y_amax_capacity >=
+ *   lcml_fp8_amax_parts_max(M, N) words.  The tile kernels write them from
+ *   their epilogue (one per workgroup); the other kernels are followed by
+ *   an amax pass over y.
+ * x_amax_part, x_amax_npart (optional): such partials of x (e.g. a previous
+ *   call's y_amax_part): the dynamic scale is amax/448 of their maximum,
+ *   computed without a pass over x (the fused small-M kernel still reduces
+ *   x itself; the maximum, and so every result, is the same).
+ * The results (y, x_scale_out) equal lcml_fp8_gemm_dynamic's bit for bit.
+ */
+LCML_API int64_t lcml_fp8_amax_parts_max(int64_t M, int64_t N);
+LCML_API int lcml_fp8_gemm_dynamic_ex(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
+                                      const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel,
+                                      float alpha, const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1,
+                                      float beta, int act, void *y, int y_dtype, int64_t ldy, float *x_scale_out,
+                                      const uint32_t *x_amax_part, int x_amax_npart, uint32_t *y_amax_part,
+                                      int64_t y_amax_capacity, int *y_amax_npart, void *workspace,
+                                      int64_t workspace_bytes, int kernel, void *stream);
+
+/*
  * lcml_fp8_gemm_dynamic without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops
  * that forbid allocation, harnesses that count allocations).  No counterpart

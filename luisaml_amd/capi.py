@@ -53,6 +53,10 @@ _SIGS = {
     "lcml_fp8_gemm_dynamic_workspace_bytes": (_i64, [_i64, _i64, _int]),
     "lcml_fp8_gemm_dynamic": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
                                      _f32, _int, _vp, _int, _i64, _vp, _vp, _i64, _int, _vp]),
+    "lcml_fp8_amax_parts_max": (_i64, [_i64, _i64]),
+    "lcml_fp8_gemm_dynamic_ex": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64, _i64,
+                                        _f32, _int, _vp, _int, _i64, _vp, _vp, _int, _vp, _i64,
+                                        C.POINTER(C.c_int), _vp, _i64, _int, _vp]),
     "lcml_fp8_gemm_dynamic_noalloc": (_int, [_i64, _i64, _i64, _vp, _i64, _vp, _vp, _int, _f32, _vp, _int, _i64,
                                              _i64, _f32, _int, _vp, _int, _i64, _vp, _int, _vp]),
     "lcml_fp8_quantize_nhwc": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
@@ -264,6 +268,40 @@ def gemm_dynamic(x: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor,
                                        y.stride(0), _ptr(scale_out), _ptr(workspace), ws_bytes, int(kernel),
                                        _stream(stream)))
     return y
+
+
+def amax_parts_buffer(M: int, N: int, device) -> torch.Tensor:
+    """A device buffer for the partial maxima of an M x N output."""
+    return torch.empty(int(lib().lcml_fp8_amax_parts_max(M, N)), dtype=torch.int32, device=device)
+
+
+def gemm_dynamic_ex(x: torch.Tensor, b_packed: torch.Tensor, b_scale: torch.Tensor, N: int, K: int,
+                    c: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 1.0, act: int = ACT_NONE,
+                    out_dtype=torch.float32, kernel: int = KERNEL_AUTO, out: torch.Tensor | None = None,
+                    scale_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                    x_amax: tuple | None = None, y_amax_part: torch.Tensor | None = None, stream=None):
+    """gemm_dynamic for chains of dynamically quantised linears: x_amax =
+    (partials, count) of x from an earlier call skips the amax pass over x;
+    y_amax_part (from amax_parts_buffer) receives partials of y.  Returns
+    (y, count of y partials written, or 0)."""
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+    M = x.shape[0]
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x.device)
+    ydt = _DTYPE_CODE.get(y.dtype, 0)
+    cc, nd, c0, c1 = _c_args(c)
+    per_ch = int(b_scale.numel() > 1)
+    need = lib().lcml_fp8_gemm_dynamic_workspace_bytes(M, K, int(kernel) if x.data_ptr() % 16 == 0 else KERNEL_MFMA)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    xp, xn = (x_amax[0], int(x_amax[1])) if x_amax is not None else (None, 0)
+    npart = C.c_int(0)
+    _check(lib().lcml_fp8_gemm_dynamic_ex(M, N, K, _ptr(x), x.stride(0), _ptr(b_packed), _ptr(b_scale), per_ch,
+                                          float(alpha), _ptr(cc), nd, c0, c1, float(beta), int(act), _ptr(y), ydt,
+                                          y.stride(0), _ptr(scale_out), _ptr(xp), xn, _ptr(y_amax_part),
+                                          y_amax_part.numel() if y_amax_part is not None else 0, C.byref(npart),
+                                          _ptr(workspace), ws_bytes, int(kernel), _stream(stream)))
+    return y, npart.value
 
 
 # --------------------------------------------------------------- Conv -------

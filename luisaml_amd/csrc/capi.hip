@@ -91,6 +91,7 @@ int make_epilogue(lcml::Epilogue &e, const char *fn, int64_t M, int64_t N, const
     e.ldy = ldy;
     e.M = M;
     e.N = N;
+    e.amax_part = nullptr;
     return LCML_OK;
 }
 
@@ -223,18 +224,30 @@ int auto_gemm_kernel(int64_t M, int64_t N, int64_t K) {
 }
 }  // namespace
 
-int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda, const float *a_scale,
-                  const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
-                  const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
-                  int y_dtype, int64_t ldy, int kernel, void *stream) {
-    const char *fn = "lcml_fp8_gemm";
+namespace {
+// Amax partials of y (optional, y_amax_part non-null): the caller checked
+// y is fp32, dense (ldy == N) and the buffer holds lcml_fp8_amax_parts_max
+// words; *y_amax_npart receives the count written.
+struct YAmax {
+    uint32_t *part = nullptr;
+    int *npart = nullptr;
+};
+
+// lcml_fp8_gemm with an optional amax-partials output
+int gemm_core(const char *fn, int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda, const float *a_scale,
+              const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha, const float *c,
+              int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+              int kernel, void *stream, YAmax ya) {
     if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
                                                (long long)M, (long long)N, (long long)K);
     lcml::Epilogue e;
     if (int rc = make_epilogue(e, fn, M, N, a_scale, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
                                c_dim1, beta, act, y, y_dtype, ldy))
         return rc;
-    if (M == 0) return LCML_OK;
+    if (M == 0) {
+        if (ya.npart) *ya.npart = 0;
+        return LCML_OK;
+    }
     if (!a || !b_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
     if (K % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", fn, (long long)K);
     if (lda < K || lda % 16 != 0 || !aligned(a, 16))
@@ -255,9 +268,18 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
             return fail(LCML_ERR_UNSUPPORTED, "%s: operand larger than 2 GiB for the MFMA kernel", fn);
         if ((M + 127) / 128 * ((N + 127) / 128) >= (int64_t)0x80000000)
             return fail(LCML_ERR_UNSUPPORTED, "%s: M=%lld N=%lld exceeds the tile grid", fn, (long long)M, (long long)N);
+        if (ya.part) {  // the tile kernels write one partial per workgroup
+            e.amax_part = ya.part;
+            *ya.npart = (int)lcml::gemm_mfma_workgroups(
+                M, N, kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8);
+        }
         err = lcml::launch_gemm_mfma(M, N, K, a, lda, b_packed, e,
                                      kernel == LCML_KERNEL_MFMA || kernel == LCML_KERNEL_MFMA_128, s,
                                      kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8);
+        if (ya.part) label = kernel == LCML_KERNEL_MFMA_128 || kernel == LCML_KERNEL_MFMA_128_FP8
+                                 ? (kernel == LCML_KERNEL_MFMA_128 ? "gemm_mfma_128_amax" : "gemm_mfma_128_fp8_amax")
+                                 : (kernel == LCML_KERNEL_MFMA ? "gemm_mfma_256_amax" : "gemm_mfma_256_fp8_amax");
+        ya.part = nullptr;  // written
         break;
     case LCML_KERNEL_SKINNY:
     case LCML_KERNEL_SKINNY_FP8:
@@ -272,7 +294,27 @@ int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda
     case LCML_KERNEL_VALU: err = lcml::launch_gemv_valu_fp8(M, N, K, a, lda, b_packed, e, s); break;
     default: return fail(LCML_ERR_INVALID_ARG, "%s: unknown kernel %d", fn, kernel);
     }
-    return hip_status(err, fn, label);
+    if (int rc = hip_status(err, fn, label)) return rc;
+    if (ya.part)  // kernels without the epilogue partials: an amax pass over y
+        return hip_status(lcml::launch_amax_partials(static_cast<const float *>(y), M * N, ya.part, ya.npart, s),
+                          fn, "amax_partials");
+    return LCML_OK;
+}
+}  // namespace
+
+int lcml_fp8_gemm(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda, const float *a_scale,
+                  const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
+                  const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
+                  int y_dtype, int64_t ldy, int kernel, void *stream) {
+    return gemm_core("lcml_fp8_gemm", M, N, K, a, lda, a_scale, b_packed, b_scale, b_scale_per_channel, alpha, c,
+                     c_ndim, c_dim0, c_dim1, beta, act, y, y_dtype, ldy, kernel, stream, YAmax{});
+}
+
+int64_t lcml_fp8_amax_parts_max(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0) return 0;
+    const int64_t tiles = lcml::gemm_mfma_workgroups(M, N, true);  // 128x128 tiles: the most workgroups
+    const int64_t pass = lcml::amax_partials_count(M * N);
+    return tiles > pass ? tiles : pass;
 }
 
 namespace {
@@ -305,32 +347,49 @@ int64_t lcml_fp8_gemm_dynamic_workspace_bytes(int64_t M, int64_t K, int kernel) 
 namespace {
 // lcml_fp8_gemm_dynamic with the workspace resolved by the caller: the
 // caller's buffer, or the no-allocation entry point's device array.
+// x partial maxima given (x_amax_part, x_amax_npart > 0): the two-step path
+// encodes from them instead of an amax pass over x (the fused small-M
+// kernel computes the same maximum itself)
+struct XAmax {
+    const uint32_t *part = nullptr;
+    int npart = 0;
+};
+
 int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
                       const uint8_t *b_packed, const float *b_scale, int b_scale_per_channel, float alpha,
                       const float *c, int c_ndim, int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y,
                       int y_dtype, int64_t ldy, float *x_scale_out, void *workspace, int64_t workspace_bytes,
-                      int kernel, void *stream) {
+                      int kernel, void *stream, XAmax xa = XAmax{}, YAmax ya = YAmax{}) {
     if (M < 0 || N <= 0 || K <= 0) return fail(LCML_ERR_INVALID_ARG, "%s: M=%lld N=%lld K=%lld", fn,
                                                (long long)M, (long long)N, (long long)K);
     lcml::Epilogue e;
     if (int rc = make_epilogue(e, fn, M, N, nullptr, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
                                c_dim1, beta, act, y, y_dtype, ldy))
         return rc;
-    if (M == 0) return LCML_OK;
+    if (M == 0) {
+        if (ya.npart) *ya.npart = 0;
+        return LCML_OK;
+    }
     if (!x || !b_packed) return fail(LCML_ERR_INVALID_ARG, "%s: NULL operand", fn);
     if (K % 16 != 0) return fail(LCML_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", fn, (long long)K);
     if (ldx < K) return fail(LCML_ERR_INVALID_ARG, "%s: ldx=%lld < K=%lld", fn, (long long)ldx, (long long)K);
     if (!aligned(b_packed, 16)) return fail(LCML_ERR_INVALID_ARG, "%s: b_packed not 16-byte aligned", fn);
     hipStream_t s = (hipStream_t)stream;
-    if (dynamic_fusable(M, K, x, ldx, kernel))
-        return hip_status(lcml::launch_gemm_skinny_dynamic(M, N, K, x, ldx, b_packed, e, x_scale_out,
-                                                           kernel != LCML_KERNEL_SKINNY_FP8 &&
-                                                               kernel != LCML_KERNEL_AUTO_FP8,
-                                                           s),
-                          fn,
-                          kernel == LCML_KERNEL_SKINNY_FP8 || kernel == LCML_KERNEL_AUTO_FP8
-                              ? "gemm_skinny_dynamic_fp8"
-                              : "gemm_skinny_dynamic");
+    if (dynamic_fusable(M, K, x, ldx, kernel)) {
+        if (int rc = hip_status(lcml::launch_gemm_skinny_dynamic(M, N, K, x, ldx, b_packed, e, x_scale_out,
+                                                                 kernel != LCML_KERNEL_SKINNY_FP8 &&
+                                                                     kernel != LCML_KERNEL_AUTO_FP8,
+                                                                 s),
+                                fn,
+                                kernel == LCML_KERNEL_SKINNY_FP8 || kernel == LCML_KERNEL_AUTO_FP8
+                                    ? "gemm_skinny_dynamic_fp8"
+                                    : "gemm_skinny_dynamic"))
+            return rc;
+        if (ya.part)
+            return hip_status(lcml::launch_amax_partials(static_cast<const float *>(y), M * N, ya.part, ya.npart, s),
+                              fn, "amax_partials");
+        return LCML_OK;
+    }
     // two-step path: quantise into the workspace, then the selected GEMM.
     // The size is that of this path whatever the size query said: the query
     // cannot see x, and a misaligned x takes this path where an aligned one
@@ -344,10 +403,11 @@ int gemm_dynamic_impl(const char *fn, int64_t M, int64_t N, int64_t K, const flo
     uint8_t *q = ws;
     uint32_t *part = reinterpret_cast<uint32_t *>(ws + pad256(M * K));
     float *scale = x_scale_out ? x_scale_out : reinterpret_cast<float *>(ws + pad256(M * K) + LCML_FP8_DYNAMIC_WORKSPACE_BYTES);
-    hipError_t err = lcml::launch_quantize_dynamic(x, q, M * K, scale, part, s);
-    if (int rc = hip_status(err, fn, "quantize_dynamic")) return rc;
-    return lcml_fp8_gemm(M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
-                         c_dim1, beta, act, y, y_dtype, ldy, kernel, stream);
+    hipError_t err = xa.part ? lcml::launch_quantize_dynamic_parts(x, q, M * K, xa.part, xa.npart, scale, s)
+                             : lcml::launch_quantize_dynamic(x, q, M * K, scale, part, s);
+    if (int rc = hip_status(err, fn, xa.part ? "quantize_dynamic_parts" : "quantize_dynamic")) return rc;
+    return gemm_core(fn, M, N, K, q, K, scale, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                     c_dim1, beta, act, y, y_dtype, ldy, kernel, stream, ya);
 }
 
 // The no-allocation variant's workspace: one array per device, in device
@@ -389,6 +449,35 @@ int lcml_fp8_gemm_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64
     return gemm_dynamic_impl("lcml_fp8_gemm_dynamic", M, N, K, x, ldx, b_packed, b_scale, b_scale_per_channel, alpha,
                              c, c_ndim, c_dim0, c_dim1, beta, act, y, y_dtype, ldy, x_scale_out, workspace,
                              workspace_bytes, kernel, stream);
+}
+
+int lcml_fp8_gemm_dynamic_ex(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx, const uint8_t *b_packed,
+                             const float *b_scale, int b_scale_per_channel, float alpha, const float *c, int c_ndim,
+                             int64_t c_dim0, int64_t c_dim1, float beta, int act, void *y, int y_dtype, int64_t ldy,
+                             float *x_scale_out, const uint32_t *x_amax_part, int x_amax_npart, uint32_t *y_amax_part,
+                             int64_t y_amax_capacity, int *y_amax_npart, void *workspace, int64_t workspace_bytes,
+                             int kernel, void *stream) {
+    const char *fn = "lcml_fp8_gemm_dynamic_ex";
+    XAmax xa;
+    if (x_amax_part) {
+        if (x_amax_npart < 1) return fail(LCML_ERR_INVALID_ARG, "%s: x_amax_npart=%d", fn, x_amax_npart);
+        xa.part = x_amax_part;
+        xa.npart = x_amax_npart;
+    }
+    YAmax ya;
+    if (y_amax_part) {
+        if (y_dtype != LCML_DTYPE_FLOAT || ldy != N)
+            return fail(LCML_ERR_UNSUPPORTED, "%s: amax partials of y need a dense fp32 y (ldy == N)", fn);
+        if (!y_amax_npart) return fail(LCML_ERR_INVALID_ARG, "%s: y_amax_npart is NULL", fn);
+        if (y_amax_capacity < lcml_fp8_amax_parts_max(M, N))
+            return fail(LCML_ERR_INVALID_ARG, "%s: y_amax_capacity=%lld < lcml_fp8_amax_parts_max=%lld", fn,
+                        (long long)y_amax_capacity, (long long)lcml_fp8_amax_parts_max(M, N));
+        ya.part = y_amax_part;
+        ya.npart = y_amax_npart;
+    }
+    return gemm_dynamic_impl(fn, M, N, K, x, ldx, b_packed, b_scale, b_scale_per_channel, alpha, c, c_ndim, c_dim0,
+                             c_dim1, beta, act, y, y_dtype, ldy, x_scale_out, workspace, workspace_bytes, kernel,
+                             stream, xa, ya);
 }
 
 int lcml_fp8_gemm_dynamic_noalloc(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,

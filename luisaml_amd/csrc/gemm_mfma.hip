@@ -173,9 +173,11 @@ __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) 
 // software rounding) took ~19 us for a 256x256 tile's bf16 epilogue, this one
 // ~4.5 us (fp32: ~8 us); on the 4096-row transformer linears that is 6-7% of
 // the exact kernel's time and 15-18% of the native FP8 one's.
-template <int ACT, bool HAS_C, bool BF16>
+// AMAX: m accumulates max |value| over the in-range elements written (rows
+// below M, columns below N; NaN compares false and is skipped).
+template <int ACT, bool HAS_C, bool BF16, bool AMAX = false>
 __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, int64_t row0, int64_t col, bool cols_ok,
-                                         float sc0, float sc1, float cb0, float cb1) {
+                                         float sc0, float sc1, float cb0, float cb1, float &m, bool c1_ok) {
     // every operation rounds on its own, as in epi_value_cv (where alpha is
     // applied under a runtime test, so nothing fuses across it): no FMA
 #pragma clang fp contract(off)
@@ -195,6 +197,12 @@ __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, in
         }
         v0 = apply_act(v0, ACT);
         v1 = apply_act(v1, ACT);
+        if constexpr (AMAX) {
+            const bool r_ok = row0 + 2 * q < e.M;
+            const float a0 = fabsf(v0), a1 = fabsf(v1);
+            m = r_ok && cols_ok && a0 > m ? a0 : m;
+            m = r_ok && c1_ok && a1 > m ? a1 : m;
+        }
         if constexpr (BF16) {
             const f2 v = {v0, v1};
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2)), r, off,
@@ -450,11 +458,13 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint8_t *ld
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, off, 0, 0, 0);
 }
 
-template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV, bool PP, bool DIRECT = false>
+template <int WAVES_M, int WAVES_N, int WM, int WN, bool EXACT, bool CONV, bool PP, bool DIRECT = false,
+          bool AMAX = false>
 __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_gemm_mfma(GemmArgs g) {
     using T = Tile<WAVES_M, WAVES_N, WM, WN>;
     constexpr int NSTAGE = T::NST;
     static_assert(!DIRECT || (T::ONE_PER_SIMD && !CONV && !PP), "the persistent direct-store loop is the one-wavefront-per-SIMD GEMM's");
+    static_assert(!AMAX || (!CONV && !DIRECT), "amax partials: the row-major staged epilogue");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -1222,6 +1232,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // (lanes 0-31 and 32-63, 4 rows apart) fall in opposite bank halves.
         static_assert(WN % 2 == 0 && WM % 2 == 0, "32-column and 32-row block pairs");
         constexpr int ER = T::EP_ROWS;
+        float amax_m = 0.0f;  // AMAX: this lane's max |y|
         float *st = reinterpret_cast<float *>(smem) + wave * (ER * EP2_PITCH);
 #pragma unroll
         for (int jp = 0; jp < WN / 2; ++jp) {
@@ -1247,8 +1258,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         const float cb1 = e.c ? (e.beta == 1.0f ? cv1 : e.beta * cv1) : 0.0f;
         auto fast_pass = [&](const float *src, int64_t row0) {
             auto go = [&](auto act, auto has_c, auto bf) {
-                epi_rows<decltype(act)::value, decltype(has_c)::value, decltype(bf)::value>(e, src, row0, col, c0ok,
-                                                                                           sc0, sc1, cb0, cb1);
+                epi_rows<decltype(act)::value, decltype(has_c)::value, decltype(bf)::value, AMAX>(
+                    e, src, row0, col, c0ok, sc0, sc1, cb0, cb1, amax_m, c1ok);
             };
             auto by_out = [&](auto act, auto has_c) {
                 if (e.y_bf16)
@@ -1294,6 +1305,10 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                             const float2 a = *reinterpret_cast<const float2 *>(src + 2 * q * EP2_PITCH);
                             const float v0 = epi_value_cv(e, sc0, cv0, a.x), v1 = epi_value_cv(e, sc1, cv1, a.y);
                             if (row < e.M) {
+                                if constexpr (AMAX) {
+                                    amax_m = fabsf(v0) > amax_m ? fabsf(v0) : amax_m;
+                                    amax_m = c1ok && fabsf(v1) > amax_m ? fabsf(v1) : amax_m;
+                                }
                                 if (pair) {
                                     epi_store2(e, row, col, v0, v1);
                                 } else {
@@ -1309,8 +1324,10 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                             if (row >= e.M) break;
                             const float2 a = *reinterpret_cast<const float2 *>(src + 2 * q * EP2_PITCH);
                             const float v0 = epi_value(e, sc0, row, col, a.x);
+                            if constexpr (AMAX) amax_m = fabsf(v0) > amax_m ? fabsf(v0) : amax_m;
                             if (c1ok) {
                                 const float v1 = epi_value(e, sc1, row, col + 1, a.y);
+                                if constexpr (AMAX) amax_m = fabsf(v1) > amax_m ? fabsf(v1) : amax_m;
                                 if (pair) {
                                     epi_store2(e, row, col, v0, v1);
                                 } else {
@@ -1326,6 +1343,20 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             }
             __syncthreads();
         }
+        }
+        if constexpr (AMAX) {
+            // the workgroup's partial: a wavefront max, then the wavefronts'
+            // through LDS (free after the last pass's barrier)
+            const float wm_max = wave_max(amax_m);
+            float *red = reinterpret_cast<float *>(smem);
+            if (lane == 0) red[wave] = wm_max;
+            __syncthreads();
+            if (tid == 0) {
+                float m = red[0];
+#pragma unroll
+                for (int w = 1; w < T::NW; ++w) m = red[w] > m ? red[w] : m;
+                e.amax_part[blockIdx.x] = __builtin_bit_cast(uint32_t, m);
+            }
         }
     }
 }
@@ -1364,9 +1395,10 @@ int device_cus() {
     return n;
 }
 
-template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false, bool DIRECT = false>
+template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false, bool DIRECT = false,
+          bool AMAX = false>
 hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
-    auto *fn = k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT>;
+    auto *fn = k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT, AMAX>;
     static std::atomic<uint64_t> lds_set{0};
     if (hipError_t err = ensure_dynamic_lds(reinterpret_cast<const void *>(fn), Cfg::LDS_BYTES, lds_set);
         err != hipSuccess)
@@ -1385,7 +1417,7 @@ hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
     // more), each walking tiles blockIdx.x + k * gridDim.x
     int grid = g.tiles_m * g.tiles_n;
     if constexpr (DIRECT) grid = grid < device_cus() ? grid : device_cus();
-    hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT>),
+    hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT, AMAX>),
                        dim3(grid, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES, s, g);
     return hipGetLastError();
 }
@@ -1424,6 +1456,10 @@ bool direct_epilogue_ok(const Epilogue &e) {
 template <bool EXACT, bool CONV>
 hipError_t launch(GemmArgs &g, hipStream_t s) {
     if constexpr (!CONV)
+        if (g.e.amax_part)  // fp32 outputs only (the caller's condition): the 2x4 layout
+            return launch_cfg<Shipped, WAVES_M, WAVES_N, WM, WN, EXACT, false, EXACT && (bool)LCML_GEMM_PINGPONG,
+                              false, true>(g, s);
+    if constexpr (!CONV)
         if (g.e.y_bf16 && g.N > Wide::BN) {
             if (direct_epilogue_ok(g.e) && g.K > kPackK) return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false, false, true>(g, s);
             return launch_cfg<Wide, 2, 2, 4, 4, EXACT, false>(g, s);
@@ -1439,9 +1475,18 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
     g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
     g.a_bytes = (uint32_t)((M - 1) * lda + K);
     g.e = e;
-    if (small_tiles)
+    if (small_tiles) {
+        if (e.amax_part)
+            return exact ? launch_cfg<Small, 2, 2, 2, 2, true, false, false, false, true>(g, s)
+                         : launch_cfg<Small, 2, 2, 2, 2, false, false, false, false, true>(g, s);
         return exact ? launch_cfg<Small, 2, 2, 2, 2, true, false>(g, s) : launch_cfg<Small, 2, 2, 2, 2, false, false>(g, s);
+    }
     return exact ? launch<true, false>(g, s) : launch<false, false>(g, s);
+}
+
+int64_t gemm_mfma_workgroups(int64_t M, int64_t N, bool small_tiles) {
+    const int64_t t = small_tiles ? 128 : 256;
+    return ((M + t - 1) / t) * ((N + t - 1) / t);
 }
 
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,

@@ -264,6 +264,10 @@ struct Epilogue {
     int y_bf16;
     int64_t ldy;
     int64_t M, N;
+    // the tile kernels' AMAX instantiation: one word per workgroup, the fp32
+    // bits of max |y| over the elements it stores (NaN skipped), the input
+    // of the next dynamic quantisation of y; nullptr elsewhere
+    uint32_t *amax_part;
 };
 
 // Bias under the reference Gemm broadcast rules (gemm.cpp:84-97).

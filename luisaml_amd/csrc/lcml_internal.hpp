@@ -20,6 +20,12 @@ hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream
 // partial maxima (at most kMaxAmaxPartials words at part); *npart = count
 constexpr int kMaxAmaxPartials = 1024;
 hipError_t launch_amax_partials(const float *x, int64_t n, uint32_t *part, int *npart, hipStream_t s);
+// the number of partials launch_amax_partials writes for n elements
+int amax_partials_count(int64_t n);
+// the encode half of a dynamic quantisation, from npart partial maxima
+// (fp32 bits of max |x| over parts covering x) already computed
+hipError_t launch_quantize_dynamic_parts(const float *x, uint8_t *y, int64_t n, const uint32_t *part, int npart,
+                                         float *scale_out, hipStream_t s);
 hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float *scale_out,
                                    uint32_t *work, hipStream_t s);
 hipError_t launch_amax_to_float(const uint32_t *amax_bits, float *out, hipStream_t s);
@@ -35,6 +41,9 @@ hipError_t launch_unpack_weight(const uint8_t *packed, int64_t K, int64_t N, int
 hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                             const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s,
                             bool small_tiles = false);
+// workgroups of a non-persistent tile GEMM launch (one per tile): with
+// e.amax_part set, the number of partial maxima it writes
+int64_t gemm_mfma_workgroups(int64_t M, int64_t N, bool small_tiles);
 // implicit-im2col FP8 convolution on the MFMA tile kernel: x_nhwc E4M3
 // [Nb][H][W][C] ((C/group) % 16 == 0), bp = conv weights packed per group
 // with K = (kh, kw, c), output NCHW [Nb][Cout][OH][OW] through the epilogue

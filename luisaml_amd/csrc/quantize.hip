@@ -343,13 +343,17 @@ hipError_t launch_amax(const float *x, int64_t n, uint32_t *amax_bits, hipStream
     return hipGetLastError();
 }
 
-hipError_t launch_amax_partials(const float *x, int64_t n, uint32_t *part, int *npart, hipStream_t s) {
+int amax_partials_count(int64_t n) {
     // one workgroup per CU at most (grid-stride beyond), which measured
     // faster than 512 or 1024 workgroups on 16M-45M element tensors
     constexpr int64_t kGrid = 256;
     static_assert(kGrid <= kMaxAmaxPartials, "partials fit the workspace");
     int64_t g = (n / 4 + (int64_t)kAmaxThreads * kAmaxU - 1) / ((int64_t)kAmaxThreads * kAmaxU);
-    g = g < 1 ? 1 : (g > kGrid ? kGrid : g);
+    return (int)(g < 1 ? 1 : (g > kGrid ? kGrid : g));
+}
+
+hipError_t launch_amax_partials(const float *x, int64_t n, uint32_t *part, int *npart, hipStream_t s) {
+    const int64_t g = amax_partials_count(n);
     *npart = (int)g;
     hipLaunchKernelGGL(k_amax_partials, dim3((unsigned)g), dim3(kAmaxThreads), 0, s, x, n, part);
     return hipGetLastError();
@@ -382,13 +386,18 @@ hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float 
     int npart = 0;
     hipError_t err = launch_amax_partials(x, n, work, &npart, s);
     if (err != hipSuccess) return err;
+    return launch_quantize_dynamic_parts(x, y, n, work, npart, scale_out, s);
+}
+
+hipError_t launch_quantize_dynamic_parts(const float *x, uint8_t *y, int64_t n, const uint32_t *part, int npart,
+                                         float *scale_out, hipStream_t s) {
     const int64_t n4 = (aligned16(x) && aligned4(y)) ? n / 4 : 0;
     if (n4)
         hipLaunchKernelGGL(k_quantize_vec<true>, dim3(grid_vec(n4, kU)), dim3(kThreads), 0, s, x, y, n4, (int64_t)1,
-                           n, nullptr, work, npart, scale_out);
+                           n, nullptr, part, npart, scale_out);
     if (n4 * 4 < n)
         hipLaunchKernelGGL(k_quantize_scalar<true>, dim3(grid_for(n - n4 * 4)), dim3(kThreads), 0, s, x, y,
-                           n4 * 4, n, (int64_t)1, n, nullptr, work, npart, n4 ? nullptr : scale_out);
+                           n4 * 4, n, (int64_t)1, n, nullptr, part, npart, n4 ? nullptr : scale_out);
     return hipGetLastError();
 }
 

@@ -181,3 +181,27 @@ def test_auto_fp8_is_accepted_where_auto_is():
     assert conv(capi.KERNEL_AUTO) == capi.OK
     assert conv(capi.KERNEL_AUTO_FP8) == capi.OK
     assert conv(capi.KERNEL_SKINNY) == capi.ERR_UNSUPPORTED and "AUTO_FP8" in capi.last_error()
+
+
+def test_dynamic_gemm_ex_validates_amax_partials_before_any_launch():
+    """lcml_fp8_gemm_dynamic_ex: partials of y need a dense fp32 y and a
+    buffer of lcml_fp8_amax_parts_max words, partials of x a positive count;
+    everything is rejected before a launch (this runs without a GPU)."""
+    import ctypes as C
+    L = capi.lib()
+    M, N, K = 512, 1000, 256
+    cap = L.lcml_fp8_amax_parts_max(M, N)
+    assert cap >= 4 * 8 and cap >= (M + 127) // 128 * ((N + 127) // 128)
+    assert L.lcml_fp8_amax_parts_max(0, N) == 0
+    n = C.c_int(-5)
+
+    def call(y_dtype=1, ldy=N, ypart=0x3000, capv=cap, npart=C.byref(n), xpart=None, xn=0, m=M):
+        return L.lcml_fp8_gemm_dynamic_ex(m, N, K, 0x1000, K, 0x1000, 0x1000, 0, 1.0, None, 0, 0, 0, 1.0, 0,
+                                          0x2000, y_dtype, ldy, None, xpart, xn, ypart, capv, npart, None, 0, 0, None)
+
+    assert call(y_dtype=16) == capi.ERR_UNSUPPORTED and "fp32" in capi.last_error()
+    assert call(ldy=N + 8) == capi.ERR_UNSUPPORTED
+    assert call(capv=cap - 1) == capi.ERR_INVALID_ARG and "capacity" in capi.last_error()
+    assert call(npart=None) == capi.ERR_INVALID_ARG
+    assert call(ypart=None, xpart=0x4000, xn=0) == capi.ERR_INVALID_ARG
+    assert call(m=0) == capi.OK and n.value == 0  # nothing to do: no partials

@@ -211,6 +211,19 @@ def test_transformer_down_projection_from_gelu_output(dev, block_input):
     qh, shd = capi.quantize_dynamic(h)
     full_matrix_check(y, qh.view(4096, 11008), shd, capi.unpack_weight(bp, 11008, 4096, w_is_nk=False), d_sw,
                       bias=to_dev(bias, dev))
+    # the chained form the benchmark runs: the up-projection's epilogue writes
+    # the partial maxima of its output, and the down-projection quantises
+    # from them without an amax pass -- the same scale and output, bit for bit
+    part = capi.amax_parts_buffer(4096, 11008, dev)
+    h2, n = capi.gemm_dynamic_ex(to_dev(x, dev), bp_up, d_sw_up, 11008, 4096, c=to_dev(b_up, dev),
+                                 act=capi.ACT_GELU_ERF, y_amax_part=part)
+    assert torch.equal(h2.view(torch.int32), h.view(torch.int32))
+    assert part[:n].cpu().numpy().view(np.float32).max() == np.abs(h_host).max()
+    s2 = torch.empty(1, device=dev)
+    y2, _ = capi.gemm_dynamic_ex(h2, bp, d_sw, 4096, 11008, c=to_dev(bias, dev), out_dtype=torch.float32,
+                                 scale_out=s2, x_amax=(part, n))
+    assert s2.cpu().numpy().view(np.uint32)[0] == sh_ref.view(np.uint32)
+    assert torch.equal(y2.view(torch.int32), y.view(torch.int32))
 
 
 NATIVE_FROB = 3e-5  # documented relative Frobenius error of the native FP8 MFMA kernels (block truncation)
