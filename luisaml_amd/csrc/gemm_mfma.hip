@@ -137,6 +137,10 @@ struct GemmArgs {
     uint32_t a_bytes, b_bytes;  // buffer extents for range checking
     int tiles_m, tiles_n;
     int nk;           // K steps of 128
+    // row slices (the conv's 2x4 layout on a grid of one tile column): tiles
+    // 0 .. slice_first-1 are whole BM-row tiles, the ones after them
+    // slice_rows rows each (a multiple of 32, below BM); 0: no slices
+    int slice_first, slice_rows;
     Epilogue e;
 };
 
@@ -487,6 +491,33 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     };
     int64_t m0, n0;
     tile_origin(blockIdx.x, m0, n0);
+    // Row slices (SLICE, when the launcher sets them): workgroup t below
+    // slice_first takes rows t*BM .. (the ids in order: the first round of
+    // workgroups fills every CU with whole tiles), a later one slice_rows
+    // rows after them.  A tile of L 32-row blocks gives wave row 0 the first
+    // ceil(L/2) blocks and wave row 1 the rest (4 and 4 in a whole tile), so
+    // the two wavefronts that share a SIMD split a slice's blocks evenly;
+    // each wavefront's loop runs MFMAs for its own blocks only.
+    constexpr bool SLICE = CONV && WAVES_M == 2 && WM == 4 && !T::ONE_PER_SIMD;
+    int tile_rows = T::BM;
+    if constexpr (SLICE)
+        if (g.slice_rows) {
+            // within each part, ids regrouped so that each XCD (id % 8)
+            // takes one contiguous range of rows, as tile_origin does
+            // (slice_first is a multiple of 8, so id % 8 = part id % 8)
+            const int t = (int)blockIdx.x, first = g.slice_first;
+            const bool whole = t < first;
+            const int s = whole ? t : t - first, cnt = whole ? first : (int)gridDim.x - first;
+            const int q = cnt >> 3, r = cnt & 7, x = s & 7;
+            const int idx = x * q + (x < r ? x : r) + (s >> 3);
+            m0 = whole ? (int64_t)idx * T::BM : (int64_t)first * T::BM + (int64_t)idx * g.slice_rows;
+            n0 = 0;
+            tile_rows = whole ? T::BM : g.slice_rows;
+        }
+    const int live0 = (tile_rows / 32 + 1) / 2;  // 32-row blocks of wave row 0 (WM in a whole tile)
+    // this wavefront's blocks and first row in the tile (wave-uniform)
+    const int wlive = SLICE ? __builtin_amdgcn_readfirstlane(wm ? tile_rows / 32 - live0 : live0) : WM;
+    const int wrow0 = SLICE ? __builtin_amdgcn_readfirstlane(wm ? live0 * 32 : 0) : wm * WM * 32;
 
     // ---- global -> LDS block assignment ----------------------------------
     // A: 1 KB block b holds rows (1024/BK)*b ..; B: block b holds panel b/CPR,
@@ -497,12 +528,16 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     const __amdgpu_buffer_rsrc_t b_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)(g.bp + (size_t)grp * g.b_bytes), 0, (int)g.b_bytes, 0x00020000);
     uint32_t a_off[T::A_BLK];
-    int a_kc[T::A_BLK];
+    // the lane's 16-byte k-chunk within a step's 64 bytes: the same for every
+    // A block (the chunk swizzle of row (wave*A_BLK + i)*16 + lane/4 depends
+    // only on (lane/16) % 4)
+    int a_kc = 0;
     uint32_t a_klim[CONV ? 1 : T::A_BLK];  // K for rows in range, 0 for rows past M
     uint32_t b_off[T::B_BLK];
     int a_ih0[CONV ? T::A_BLK : 1], a_iw0[CONV ? T::A_BLK : 1];  // CONV: top-left input pixel of the row
-    // CONV: where the block's chunk of the next step to issue lies in (kh, kw, c)
-    int a_c[CONV ? T::A_BLK : 1], a_kw[CONV ? T::A_BLK : 1], a_kh[CONV ? T::A_BLK : 1];
+    // CONV: where the lane's chunk of the next step to issue lies in (kh, kw,
+    // c), the same for every block
+    int a_c = 0, a_kw = 0, a_kh = 0;
     // the load offsets of the tile at (m0, n0); valid = false: every load
     // out of range (a persistent workgroup past its last tile)
     // (ln, wv: the lane and wavefront index; the persistent kernel passes a
@@ -514,32 +549,35 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     for (int i = 0; i < T::A_BLK; ++i) {
         const int r = (wave * T::A_BLK + i) * (1024 / BK) + lane / CPR;
         const int c = (lane % CPR) ^ a_swz(r);
-        a_kc[i] = c * 16;
+        if (i == 0) a_kc = c * 16;
         if constexpr (CONV) {
-            // a_off = the row's image base n*H*W*C; rows past M get an input
-            // pixel that is out of range for every tap
+            // a_off = the row's image base n*H*W*C; rows past M (or past a
+            // slice's rows) get an input pixel that is out of range for
+            // every tap
             const ConvGeom &cv = g.cv;
             const int64_t m = m0 + r;
             const uint32_t ohw = (uint32_t)(cv.OH * cv.OW);
             const uint32_t mm = m < g.M ? (uint32_t)m : 0u;
             const uint32_t n = mm / ohw, pix = mm - n * ohw, oh = pix / (uint32_t)cv.OW, ow = pix - oh * (uint32_t)cv.OW;
             a_off[i] = n * (uint32_t)(cv.H * cv.W * cv.Ctot) + (uint32_t)(grp * cv.Cg);
-            a_ih0[i] = m < g.M ? (int)oh * cv.sh - cv.ph : -(1 << 30);
+            a_ih0[i] = r < tile_rows && m < g.M ? (int)oh * cv.sh - cv.ph : -(1 << 30);
             a_iw0[i] = (int)ow * cv.sw - cv.pw;
-            // step 0 starts at k = c*16 < 64 <= ... ; c*16 may still exceed C
-            // (C >= 16), so normalise once
-            int cc = c * 16, kw = 0, kh = 0;
-            while (cc >= cv.Cg) {
-                cc -= cv.Cg;
-                if (++kw == cv.KW) { kw = 0; ++kh; }
-            }
-            a_c[i] = cc; a_kw[i] = kw; a_kh[i] = kh;
         } else {
             // 32-bit: the host keeps (M - 1) * lda + K below 2^31
             const bool in = (int)m0 + r < (int)g.M;
             a_off[i] = valid && in ? ((uint32_t)m0 + (uint32_t)r) * (uint32_t)g.lda + (uint32_t)(c * 16) : OOB;
             a_klim[i] = in ? (uint32_t)g.K : 0u;
         }
+    }
+    if constexpr (CONV) {
+        // step 0 starts at k = a_kc < 64; a_kc may still exceed C (C >= 16),
+        // so normalise once
+        int cc = a_kc, kw = 0, kh = 0;
+        while (cc >= g.cv.Cg) {
+            cc -= g.cv.Cg;
+            if (++kw == g.cv.KW) { kw = 0; ++kh; }
+        }
+        a_c = cc; a_kw = kw; a_kh = kh;
     }
 #pragma unroll
     for (int i = 0; i < T::B_BLK; ++i) {
@@ -552,30 +590,34 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     auto issue_tile = [&](int kt, int stage) {
         uint8_t *sa = smem + stage * T::STAGE;
         const uint32_t kbyte = (uint32_t)kt * BK;
+        // CONV: k = kbyte + chunk -> (kh, kw, c), tracked incrementally:
+        // steps are issued in order, each advancing k by BK; C % 16 == 0
+        // keeps every 16-byte chunk inside one tap
+        // (CONV: k < K exactly when the chunk's tap row kh is below KH)
+        const bool k_ok = CONV ? a_kh < g.cv.KH : (int64_t)(kbyte + (uint32_t)a_kc) < g.K;
+        const int dih = CONV ? a_kh * g.cv.dh : 0, diw = CONV ? a_kw * g.cv.dw : 0;
 #pragma unroll
         for (int i = 0; i < T::A_BLK; ++i) {
             uint32_t off;
             if constexpr (CONV) {
-                // k = kbyte + chunk -> (kh, kw, c), tracked incrementally:
-                // steps are issued in order, each advancing k by BK; C % 16
-                // == 0 keeps every 16-byte chunk inside one tap
                 const ConvGeom &cv = g.cv;
-                const uint32_t k = kbyte + (uint32_t)a_kc[i];
-                const int ih = a_ih0[i] + a_kh[i] * cv.dh, iw = a_iw0[i] + a_kw[i] * cv.dw;
-                const bool ok = (int64_t)k < g.K && (uint32_t)ih < (uint32_t)cv.H && (uint32_t)iw < (uint32_t)cv.W;
+                const int ih = a_ih0[i] + dih, iw = a_iw0[i] + diw;
+                const bool ok = k_ok && (uint32_t)ih < (uint32_t)cv.H && (uint32_t)iw < (uint32_t)cv.W;
                 off = ok ? a_off[i] + ((uint32_t)ih * (uint32_t)cv.W + (uint32_t)iw) * (uint32_t)cv.Ctot +
-                               (uint32_t)a_c[i]
+                               (uint32_t)a_c
                          : OOB;
-                a_c[i] += BK;
-                while (a_c[i] >= cv.Cg) {
-                    a_c[i] -= cv.Cg;
-                    if (++a_kw[i] == cv.KW) { a_kw[i] = 0; ++a_kh[i]; }
-                }
             } else {
-                off = kbyte + (uint32_t)a_kc[i] < a_klim[i] ? a_off[i] + kbyte : OOB;
+                off = kbyte + (uint32_t)a_kc < a_klim[i] ? a_off[i] + kbyte : OOB;
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(sa + (wave * T::A_BLK + i) * 1024), 16,
                                                      off, 0, 0, 0);
+        }
+        if constexpr (CONV) {
+            a_c += BK;
+            while (a_c >= g.cv.Cg) {
+                a_c -= g.cv.Cg;
+                if (++a_kw == g.cv.KW) { a_kw = 0; ++a_kh; }
+            }
         }
 #pragma unroll
         for (int i = 0; i < T::B_BLK; ++i) {
@@ -598,7 +640,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int kgrp = (lane >> 5) * 2;  // first k-chunk of this lane within a 64-k block
-    const int a_r0 = wm * WM * 32 + (lane & 31);
+    const int a_r0 = wrow0 + (lane & 31);
     int b_off_lds[WN];
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
@@ -627,102 +669,23 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     const uint8_t *stage0 = smem;
     auto stage_a = [&](int kt) { return stage0 + (kt % NSTAGE) * T::STAGE; };
     // one 16-byte k-chunk (chunk index c of the step) of every A and B block
-    auto read_chunk = [&](u4 (&fa)[WM], u4 (&fb)[WN], int kt, int c) {
+    // (the first NA of the A blocks: a wavefront's live ones)
+    auto read_chunk = [&](u4 (&fa)[WM], u4 (&fb)[WN], int kt, int c, auto na) {
         const uint8_t *sa = stage_a(kt), *sb = sa + T::A_BYTES;
 #pragma unroll
         for (int j = 0; j < WN; ++j) fb[j] = *reinterpret_cast<const u4 *>(sb + b_off_lds[j] + c * 1024);
+        // rows a_r0 + 32i share one chunk swizzle (a_swz depends on r/4 mod
+        // 4), so the blocks lie 32*BK bytes apart from one per-lane base
+        const uint8_t *pa = sa + a_lds_off(a_r0, c);
 #pragma unroll
-        for (int i = 0; i < WM; ++i) fa[i] = *reinterpret_cast<const u4 *>(sa + a_lds_off(a_r0 + i * 32, c));
+        for (int i = 0; i < decltype(na)::value; ++i) fa[i] = *reinterpret_cast<const u4 *>(pa + i * 32 * BK);
     };
 
 #pragma unroll
     for (int p = 0; p < NSTAGE - 1; ++p) issue_tile(p, p);
     step_sync(First{});  // tile 0
 
-    if constexpr (PP) {
-        // Ping-pong: the two wavefronts on each SIMD (row halves wm = 0 and
-        // wm = 1; wavefront w runs on SIMD w % 4) take turns.  A phase ends
-        // at a workgroup barrier; in each phase one group issues its share of
-        // a tile's global->LDS loads and reads its fragments of the next
-        // step from LDS (the memory phase) while the other group only issues
-        // matrix-core instructions on fragments it already holds (the
-        // compute phase), so the SIMD's MFMA pipe is fed from registers
-        // while the LDS serves the other wavefront.  Group 1 runs one phase
-        // behind group 0 (one extra barrier at its start, one at group 0's
-        // end: both execute 2*nk + 1 barriers).
-        //   phase 2m:   group 0 memory (step m),  group 1 compute (step m-1)
-        //   phase 2m+1: group 0 compute (step m), group 1 memory (step m)
-        // Memory phase of step m: issue tile m+NSTAGE-1 into the stage of
-        // tile m-1 (read by both groups in phases 2m-2 and 2m-1, whose reads
-        // completed before those phases' barriers), read tile m, wait for
-        // the reads (lgkmcnt(0)).  Every phase ends with vmcnt((NSTAGE-2) *
-        // LOADS): a wavefront that has issued tiles up to m+NSTAGE-1 then
-        // holds tiles <= m+1, so at the barrier closing phase 2m+1 every
-        // wavefront's share of tile m+1 has landed, before group 0 reads it
-        // in phase 2m+2.
-        const bool second = wm != 0;  // wavefront-uniform
-        auto phase_end = [&](bool lds_reads) {
-            // nothing of the phase may sink below its barrier (MFMAs do not
-            // touch memory, so the asm's memory clobber alone does not hold them)
-            __builtin_amdgcn_sched_barrier(0);
-            if (lds_reads) __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(First::value) : "memory");
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        u4 fa[WM][2], fb[WN][2];
-        if (second) {
-            asm volatile("s_barrier" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        for (int m = 0; m < g.nk; ++m) {
-            issue_tile(m + NSTAGE - 1, (m + NSTAGE - 1) % NSTAGE);
-            {
-                u4 ta[WM], tb[WN];
-                read_chunk(ta, tb, m, kgrp);
-#pragma unroll
-                for (int i = 0; i < WM; ++i) fa[i][0] = ta[i];
-#pragma unroll
-                for (int j = 0; j < WN; ++j) fb[j][0] = tb[j];
-                read_chunk(ta, tb, m, kgrp + 1);
-#pragma unroll
-                for (int i = 0; i < WM; ++i) fa[i][1] = ta[i];
-#pragma unroll
-                for (int j = 0; j < WN; ++j) fb[j][1] = tb[j];
-            }
-            phase_end(true);
-            if constexpr (EXACT) {
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        bf16x8 a16[WM], b16[WN];
-#pragma unroll
-                        for (int i = 0; i < WM; ++i)
-                            a16[i] = h ? e4m3x8_to_bf16(fa[i][c].z, fa[i][c].w) : e4m3x8_to_bf16(fa[i][c].x, fa[i][c].y);
-#pragma unroll
-                        for (int j = 0; j < WN; ++j)
-                            b16[j] = h ? e4m3x8_to_bf16(fb[j][c].z, fb[j][c].w) : e4m3x8_to_bf16(fb[j][c].x, fb[j][c].y);
-#pragma unroll
-                        for (int i = 0; i < WM; ++i)
-#pragma unroll
-                            for (int j = 0; j < WN; ++j)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
-                    }
-            } else {
-#pragma unroll
-                for (int i = 0; i < WM; ++i)
-#pragma unroll
-                    for (int j = 0; j < WN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                            join(fa[i][0], fa[i][1]), join(fb[j][0], fb[j][1]), acc[i][j], 0, 0, 0, 0, 0, 0);
-            }
-            phase_end(false);
-        }
-        if (!second) {
-            asm volatile("s_barrier" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    } else if constexpr (!CONV && T::ONE_PER_SIMD) {
+    if constexpr (!CONV && T::ONE_PER_SIMD) {
         // One wavefront per SIMD (2x2 wavefronts of 128x128): a step reads
         // 64 KB of fragments from the LDS instead of the 2x4 layout's 96 KB,
         // and the exact instantiation widens 128 instead of 192 fragment
@@ -793,7 +756,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 // the lane's k-chunk a_kc is the same for every row block
                 // (a_swz of row (wave*A_BLK + l)*16 + lane/4 is (lane/16) % 4)
                 uint32_t off = a_off[l] + kbyte;
-                if (checked) off = kbyte + (uint32_t)a_kc[0] < (uint32_t)g.K ? off : OOB;
+                if (checked) off = kbyte + (uint32_t)a_kc < (uint32_t)g.K ? off : OOB;
                 lds_load16(a_rsrc, lst + (wave_u * T::A_BLK + l) * 1024, off);
             } else {
                 // past the last step (checked steps only): out of range, as in issue_tile
@@ -1047,6 +1010,96 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 step(f1, f0, kt + 1, rso, lso, true, No{}, No{}); adv();
             }
         }
+    } else {
+    // the loops of the 2x4 and 128x128 layouts for LV live 32-row blocks
+    // of this wavefront (WM, but fewer in a slice): the others take no
+    // fragment reads, conversions or MFMAs
+    auto tile_loop = [&](auto lv) {
+    constexpr int LV = decltype(lv)::value;
+    using NA = std::integral_constant<int, LV>;
+    if constexpr (PP) {
+        // Ping-pong: the two wavefronts on each SIMD (row halves wm = 0 and
+        // wm = 1; wavefront w runs on SIMD w % 4) take turns.  A phase ends
+        // at a workgroup barrier; in each phase one group issues its share of
+        // a tile's global->LDS loads and reads its fragments of the next
+        // step from LDS (the memory phase) while the other group only issues
+        // matrix-core instructions on fragments it already holds (the
+        // compute phase), so the SIMD's MFMA pipe is fed from registers
+        // while the LDS serves the other wavefront.  Group 1 runs one phase
+        // behind group 0 (one extra barrier at its start, one at group 0's
+        // end: both execute 2*nk + 1 barriers).
+        //   phase 2m:   group 0 memory (step m),  group 1 compute (step m-1)
+        //   phase 2m+1: group 0 compute (step m), group 1 memory (step m)
+        // Memory phase of step m: issue tile m+NSTAGE-1 into the stage of
+        // tile m-1 (read by both groups in phases 2m-2 and 2m-1, whose reads
+        // completed before those phases' barriers), read tile m, wait for
+        // the reads (lgkmcnt(0)).  Every phase ends with vmcnt((NSTAGE-2) *
+        // LOADS): a wavefront that has issued tiles up to m+NSTAGE-1 then
+        // holds tiles <= m+1, so at the barrier closing phase 2m+1 every
+        // wavefront's share of tile m+1 has landed, before group 0 reads it
+        // in phase 2m+2.
+        const bool second = wm != 0;  // wavefront-uniform
+        auto phase_end = [&](bool lds_reads) {
+            // nothing of the phase may sink below its barrier (MFMAs do not
+            // touch memory, so the asm's memory clobber alone does not hold them)
+            __builtin_amdgcn_sched_barrier(0);
+            if (lds_reads) __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(First::value) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        u4 fa[WM][2], fb[WN][2];
+        if (second) {
+            asm volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int m = 0; m < g.nk; ++m) {
+            issue_tile(m + NSTAGE - 1, (m + NSTAGE - 1) % NSTAGE);
+            {
+                u4 ta[WM], tb[WN];
+                read_chunk(ta, tb, m, kgrp, NA{});
+#pragma unroll
+                for (int i = 0; i < LV; ++i) fa[i][0] = ta[i];
+#pragma unroll
+                for (int j = 0; j < WN; ++j) fb[j][0] = tb[j];
+                read_chunk(ta, tb, m, kgrp + 1, NA{});
+#pragma unroll
+                for (int i = 0; i < LV; ++i) fa[i][1] = ta[i];
+#pragma unroll
+                for (int j = 0; j < WN; ++j) fb[j][1] = tb[j];
+            }
+            phase_end(true);
+            if constexpr (EXACT) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        bf16x8 a16[WM], b16[WN];
+#pragma unroll
+                        for (int i = 0; i < LV; ++i)
+                            a16[i] = h ? e4m3x8_to_bf16(fa[i][c].z, fa[i][c].w) : e4m3x8_to_bf16(fa[i][c].x, fa[i][c].y);
+#pragma unroll
+                        for (int j = 0; j < WN; ++j)
+                            b16[j] = h ? e4m3x8_to_bf16(fb[j][c].z, fb[j][c].w) : e4m3x8_to_bf16(fb[j][c].x, fb[j][c].y);
+#pragma unroll
+                        for (int i = 0; i < LV; ++i)
+#pragma unroll
+                            for (int j = 0; j < WN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < LV; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            join(fa[i][0], fa[i][1]), join(fb[j][0], fb[j][1]), acc[i][j], 0, 0, 0, 0, 0, 0);
+            }
+            phase_end(false);
+        }
+        if (!second) {
+            asm volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
     } else if constexpr (EXACT) {
         // Each lane's 64-k fragment is two 16-byte chunks (lo: chunk kgrp,
         // hi: kgrp+1), each feeding two 32x32x16 bf16 MFMA groups (8 bytes
@@ -1059,24 +1112,24 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             for (int h = 0; h < 2; ++h) {
                 bf16x8 a16[WM], b16[WN];
 #pragma unroll
-                for (int i = 0; i < WM; ++i) a16[i] = h ? e4m3x8_to_bf16(fa[i].z, fa[i].w) : e4m3x8_to_bf16(fa[i].x, fa[i].y);
+                for (int i = 0; i < LV; ++i) a16[i] = h ? e4m3x8_to_bf16(fa[i].z, fa[i].w) : e4m3x8_to_bf16(fa[i].x, fa[i].y);
 #pragma unroll
                 for (int j = 0; j < WN; ++j) b16[j] = h ? e4m3x8_to_bf16(fb[j].z, fb[j].w) : e4m3x8_to_bf16(fb[j].x, fb[j].y);
 #pragma unroll
-                for (int i = 0; i < WM; ++i)
+                for (int i = 0; i < LV; ++i)
 #pragma unroll
                     for (int j = 0; j < WN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a16[i], b16[j], acc[i][j], 0, 0, 0);
             }
         };
-        read_chunk(lo_a, lo_b, 0, kgrp);
+        read_chunk(lo_a, lo_b, 0, kgrp, NA{});
         for (int kt = 0; kt < g.nk; ++kt) {
-            read_chunk(hi_a, hi_b, kt, kgrp + 1);
+            read_chunk(hi_a, hi_b, kt, kgrp + 1, NA{});
             __builtin_amdgcn_sched_barrier(0);
             mma_half(lo_a, lo_b);
             step_sync(Steady{});  // tile kt+1
             issue_tile(kt + NSTAGE - 1, (kt + NSTAGE - 1) % NSTAGE);
-            read_chunk(lo_a, lo_b, kt + 1, kgrp);  // past the end: an unused stage
+            read_chunk(lo_a, lo_b, kt + 1, kgrp, NA{});  // past the end: an unused stage
             __builtin_amdgcn_sched_barrier(0);
             mma_half(hi_a, hi_b);
         }
@@ -1087,20 +1140,20 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         u4 a0[WM][2], b0[WN][2], a1[WM][2], b1[WN][2];
         auto read_frag = [&](u4 (&fa)[WM][2], u4 (&fb)[WN][2], int kt) {
             u4 ta[WM], tb[WN];
-            read_chunk(ta, tb, kt, kgrp);
+            read_chunk(ta, tb, kt, kgrp, NA{});
 #pragma unroll
-            for (int i = 0; i < WM; ++i) fa[i][0] = ta[i];
+            for (int i = 0; i < LV; ++i) fa[i][0] = ta[i];
 #pragma unroll
             for (int j = 0; j < WN; ++j) fb[j][0] = tb[j];
-            read_chunk(ta, tb, kt, kgrp + 1);
+            read_chunk(ta, tb, kt, kgrp + 1, NA{});
 #pragma unroll
-            for (int i = 0; i < WM; ++i) fa[i][1] = ta[i];
+            for (int i = 0; i < LV; ++i) fa[i][1] = ta[i];
 #pragma unroll
             for (int j = 0; j < WN; ++j) fb[j][1] = tb[j];
         };
         auto mma = [&](const u4 (&fa)[WM][2], const u4 (&fb)[WN][2]) {
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
+            for (int i = 0; i < LV; ++i)
 #pragma unroll
                 for (int j = 0; j < WN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(join(fa[i][0], fa[i][1]),
@@ -1109,7 +1162,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         };
         // the step's MFMAs and the next step's fragment reads are issued
         // interleaved (sched_interleave), not as a burst of reads first
-        auto interleave = [&]() { sched_interleave<WM * WN, 2 * (WM + WN), T::LOADS>(); };
+        auto interleave = [&]() { sched_interleave<LV * WN, 2 * (LV + WN), T::LOADS>(); };
         read_frag(a0, b0, 0);
         for (int kt = 0; kt < g.nk; kt += 2) {
             step_sync(Steady{});  // tile kt+1
@@ -1123,6 +1176,18 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             mma(a1, b1);
             interleave();
         }
+    }
+    };
+    if constexpr (SLICE) {
+        switch (wlive) {
+        case 1: tile_loop(std::integral_constant<int, 1>{}); break;
+        case 2: tile_loop(std::integral_constant<int, 2>{}); break;
+        case 3: tile_loop(std::integral_constant<int, 3>{}); break;
+        default: tile_loop(std::integral_constant<int, WM>{}); break;
+        }
+    } else {
+        tile_loop(std::integral_constant<int, WM>{});
+    }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tail's loads land before the LDS is reused
     if constexpr (DIRECT) return;  // every tile's epilogue ran in the persistent loop
@@ -1171,8 +1236,10 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
 #pragma unroll 1
             for (int h = 0; h < WM / 2; ++h) {
                 const int rl = h * 64 + lane;
-                const int64_t m = m0 + wm * WM * 32 + rl;
-                if (m < e.M) {
+                const int64_t m = m0 + wrow0 + rl;
+                // the wavefront's live rows only (a slice's other rows are
+                // the next slice's)
+                if (rl < wlive * 32 && m < e.M) {
                     const uint32_t n = (uint32_t)m / ohw, pix = (uint32_t)m - n * ohw;
                     const int64_t ybase = ((int64_t)n * g.cv.CoutTot + (int64_t)grp * e.N) * ohw + pix;
                     if (inv) {
@@ -1395,6 +1462,10 @@ int device_cus() {
     return n;
 }
 
+#ifndef LCML_CONV_SLICES
+#define LCML_CONV_SLICES 1
+#endif
+
 template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false, bool DIRECT = false,
           bool AMAX = false>
 hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
@@ -1417,6 +1488,26 @@ hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
     // more), each walking tiles blockIdx.x + k * gridDim.x
     int grid = g.tiles_m * g.tiles_n;
     if constexpr (DIRECT) grid = grid < device_cus() ? grid : device_cus();
+    // The conv on the 2x4 layout, one tile column, no groups: the last round
+    // of whole tiles (one workgroup per CU) becomes slices of h rows, h the
+    // rows left over the CUs rounded up to 32 (at least 64), so that every
+    // CU takes a share of it: 100352 rows (32 images of 56x56) run as 256
+    // whole tiles, then 218 slices of 160 rows, instead of 392 whole tiles
+    // (two full rounds).
+    g.slice_first = g.slice_rows = 0;
+    if constexpr (CONV && WMv == 2 && WMb == 4 && !Cfg::ONE_PER_SIMD)
+        if (LCML_CONV_SLICES && g.tiles_n == 1 && g.cv.CoutTot == (int)g.N) {
+            const int64_t cus = device_cus();
+            const int64_t first = (int64_t)(g.tiles_m - 1) / cus * cus;  // whole tiles before the last round
+            const int64_t rem = g.M - first * Cfg::BM;                    // rows of the last round (> 0)
+            int64_t h = ((rem + cus - 1) / cus + 31) / 32 * 32;
+            h = h < 64 ? 64 : h;
+            if (h < Cfg::BM) {
+                g.slice_first = (int)first;
+                g.slice_rows = (int)h;
+                grid = (int)(first + (rem + h - 1) / h);
+            }
+        }
     hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT, AMAX>),
                        dim3(grid, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES, s, g);
     return hipGetLastError();
