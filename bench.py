@@ -439,6 +439,22 @@ def main() -> int:
             blk[name] = {"ms": round(ms, 4), "tflops": round(tf, 1),
                          "pct_fp8_peak": round(100 * tf / FP8_PEAK_TFLOPS, 1),
                          "pct_instruction_peak": round(100 * tf / peak, 1)}
+            # each linear on its own (quantisation of its input included; the
+            # down-projection's scale from the up-projection's partials of
+            # the last block above), so the block time splits by linear
+            def lin1(which, kern=kern):
+                bp_, sc_, b_ = wts[which]
+                kk, nn = shapes[which]
+                x_in, y, kw = {"qkv": (xt, y_qkv, {}), "o": (xt, y_o, {}),
+                               "up": (xt, y_up, {"act": capi.ACT_GELU_ERF, "y_amax_part": up_part}),
+                               "down": (y_up, y_dn, {"x_amax": (up_part, n_up_last[0])})}[which]
+                capi.gemm_dynamic_ex(x_in, bp_, sc_, nn, kk, c=b_, out=y, kernel=kern, workspace=ws, **kw)
+            n_up_last = [capi.gemm_dynamic_ex(xt, *wts["up"][:2], 11008, 4096, c=wts["up"][2], act=capi.ACT_GELU_ERF,
+                                              out=y_up, kernel=kern, workspace=ws, y_amax_part=up_part)[1]]
+            per = {}
+            for which in ("qkv", "o", "up", "down"):
+                per[which] = round(1e3 * timed(lambda: [lin1(which) for _ in range(n)]) / n, 1)
+            blk[name]["per_linear_us"] = per
         out["transformer_linears_m4096"] = {
             "workload": "M=4096 (batch 8 x seq 512), hidden 4096: QKV 4096->12288, O 4096->4096, up 4096->11008 "
                         "+GELU, down 11008->4096; each linear = dynamic per-tensor quantize of its fp32 input + "
