@@ -182,7 +182,10 @@ __device__ inline float wg_amax(const float *__restrict__ x, int64_t n, float *r
 #pragma unroll
         for (int u = 0; u < kAmaxU; ++u) {
             const int64_t i = i0 + (int64_t)u * kAmaxThreads;
-            v[u] = i < nv ? __builtin_nontemporal_load(x4 + i) : f4{0.f, 0.f, 0.f, 0.f};
+            // plain loads (not non-temporal): a dynamic quantisation's
+            // encode pass re-reads x at once, last-read chunks first
+            // (k_quantize_after_amax), and finds them in its XCD's L2
+            v[u] = i < nv ? x4[i] : f4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int u = 0; u < kAmaxU; ++u) {
@@ -215,6 +218,58 @@ __global__ __launch_bounds__(kAmaxThreads) void k_amax_partials(const float *__r
     __shared__ float red[kAmaxThreads / 64];
     const float m = wg_amax(x, n, red);
     if (threadIdx.x == 0) part[blockIdx.x] = f32_bits(m);
+}
+
+// The encode pass of a dynamic quantisation right after k_amax_partials, on
+// the same grid: workgroup b encodes the chunks of x that workgroup b of the
+// amax pass read (same XCD, same L2), last-read chunk first, so the tail of
+// x that is still in the L2s is read from there before it is evicted
+// (4096x4096: 29.5 -> 26.6 us for both passes, 4096x11008: 67.8 -> 62.6 us,
+// bit-identical).  Each workgroup reduces the partial maxima to the scale
+// while its first loads are in flight.  Requires x 16-byte and y 4-byte
+// aligned, n % 4 == 0 (nv = n / 4 float4 groups).
+__global__ __launch_bounds__(kAmaxThreads) void k_quantize_after_amax(const float *__restrict__ x,
+                                                                     uint8_t *__restrict__ y, int64_t nv,
+                                                                     const uint32_t *__restrict__ part, int npart,
+                                                                     float *__restrict__ scale_out) {
+    __shared__ float red[kAmaxThreads / 64];
+    const f4 *x4 = reinterpret_cast<const f4 *>(x);
+    uint32_t *y4 = reinterpret_cast<uint32_t *>(y);
+    const int64_t stride = (int64_t)gridDim.x * kAmaxThreads * kAmaxU;
+    const int64_t first = (int64_t)blockIdx.x * kAmaxThreads * kAmaxU + threadIdx.x;
+    // this thread's last chunk of the amax pass's grid-stride walk (-1: none)
+    int64_t i0 = first < nv ? first + ((nv - 1 - first) / stride) * stride : -1;
+    f4 v[kAmaxU];
+    auto load = [&](int64_t b) {
+#pragma unroll
+        for (int u = 0; u < kAmaxU; ++u) {
+            const int64_t i = b + (int64_t)u * kAmaxThreads;
+            v[u] = b >= 0 && i < nv ? x4[i] : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    load(i0);
+    const float s_tensor = scale_from_partials<kAmaxThreads>(part, npart, red);
+    if (scale_out && blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s_tensor;
+    const Recip d = make_recip(s_tensor);
+    // the scale's range test is uniform: one branch outside the loop
+    auto run = [&](auto fast) {
+        for (; i0 >= 0; i0 -= stride) {
+            uint32_t code[kAmaxU];
+#pragma unroll
+            for (int u = 0; u < kAmaxU; ++u)
+                code[u] = quantize4_t<decltype(fast)::value>(v[u].x, v[u].y, v[u].z, v[u].w, d);
+            if (i0 - stride >= 0) load(i0 - stride);
+#pragma unroll
+            for (int u = 0; u < kAmaxU; ++u) {
+                const int64_t i = i0 + (int64_t)u * kAmaxThreads;
+                if (i < nv) y4[i] = code[u];
+            }
+        }
+    };
+    if (d.fast)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 }
 
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n) {
@@ -386,6 +441,11 @@ hipError_t launch_quantize_dynamic(const float *x, uint8_t *y, int64_t n, float 
     int npart = 0;
     hipError_t err = launch_amax_partials(x, n, work, &npart, s);
     if (err != hipSuccess) return err;
+    if (n % 4 == 0 && aligned16(x) && aligned4(y)) {
+        hipLaunchKernelGGL(k_quantize_after_amax, dim3((unsigned)npart), dim3(kAmaxThreads), 0, s, x, y, n / 4, work,
+                           npart, scale_out);
+        return hipGetLastError();
+    }
     return launch_quantize_dynamic_parts(x, y, n, work, npart, scale_out, s);
 }
 

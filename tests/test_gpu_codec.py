@@ -120,7 +120,10 @@ def test_quantize_dequantize_per_axis(dev, shape, axis):
     assert_bits_equal_nan_aware(y, oracle.dequantize(ref_q, scales, axis=axis))
 
 
-@pytest.mark.parametrize("n", [1, 100, 4096, 16 * 4096, 65536, 65537, 3 << 20])
+# 3 << 20 and up: the two-pass path; 9 << 20 + 3108 walks several grid
+# strides with a ragged last chunk in the encode pass's reversed order,
+# 4096 * 4096 is a transformer linear's input
+@pytest.mark.parametrize("n", [1, 100, 4096, 16 * 4096, 65536, 65537, 3 << 20, (9 << 20) + 3108, 4096 * 4096])
 def test_quantize_dynamic_matches_oracle(dev, n):
     x = synth.normal(99 + n, (n,), std=2.5)
     q, s = capi.quantize_dynamic(to_dev(x, dev))
