@@ -55,6 +55,9 @@ namespace {
 #ifndef LCML_SKINNY_PF
 #define LCML_SKINNY_PF 1
 #endif
+#ifndef LCML_SKINNY_PRO
+#define LCML_SKINNY_PRO 1
+#endif
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every extent: loads return zeros
 constexpr int kRsrcFlags = 0x00020000;  // raw buffer resource word 3 (as the tiled GEMM uses)
@@ -280,6 +283,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         load(fr[p], kb_begin + p * UNROLL);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // DYN: one more K block in flight while the activations are quantised
+    // (consumed right after the quantisation; the ring itself stays PF deep)
+    constexpr bool PRO = DYN && LCML_SKINNY_PRO;
+    static_assert(!PRO || (PF == 1 && UNROLL == 1), "the extra block follows the ring's first");
+    Frag fx;
+    if constexpr (PRO) {
+        load(fx, kb_begin + 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     float a_dyn = 1.0f;
     if constexpr (DYN) {
         __shared__ float wmax[WAVES];
@@ -370,7 +382,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // (past the end: zeros, no memory traffic).  The scheduling barriers keep
     // each buffer's loads together and in ring order, so the wait before a
     // buffer's first use leaves the other PF-1 buffers' loads in flight.
-    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += PF * UNROLL) {
+    int kb_loop = kb_begin;
+    if constexpr (PRO) {
+        // the ring's first block, refilled two blocks ahead, then the extra one
+        read_a(fr[0], kb_begin);
+        compute(fr[0], kb_begin);
+        __builtin_amdgcn_sched_barrier(0);
+        load(fr[0], kb_begin + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(fx, kb_begin + 1);
+        compute(fx, kb_begin + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        kb_loop = kb_begin + 2;
+    }
+    for (int kb0 = kb_loop; kb0 < kb_end; kb0 += PF * UNROLL) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const int kb = kb0 + p * UNROLL;
