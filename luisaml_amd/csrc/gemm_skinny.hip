@@ -283,13 +283,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         load(fr[p], kb_begin + p * UNROLL);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // DYN: one more K block in flight while the activations are quantised
+    // DYN: PRO more K blocks in flight while the activations are quantised
     // (consumed right after the quantisation; the ring itself stays PF deep)
-    constexpr bool PRO = DYN && LCML_SKINNY_PRO;
-    static_assert(!PRO || (PF == 1 && UNROLL == 1), "the extra block follows the ring's first");
-    Frag fx;
-    if constexpr (PRO) {
-        load(fx, kb_begin + 1);
+    constexpr int PRO = DYN ? LCML_SKINNY_PRO : 0;
+    static_assert(PRO == 0 || (PF == 1 && UNROLL == 1), "the extra blocks follow the ring's first");
+    Frag fx[PRO > 0 ? PRO : 1];
+#pragma unroll
+    for (int x = 0; x < PRO; ++x) {
+        load(fx[x], kb_begin + 1 + x);
         __builtin_amdgcn_sched_barrier(0);
     }
     float a_dyn = 1.0f;
@@ -383,17 +384,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // each buffer's loads together and in ring order, so the wait before a
     // buffer's first use leaves the other PF-1 buffers' loads in flight.
     int kb_loop = kb_begin;
-    if constexpr (PRO) {
-        // the ring's first block, refilled two blocks ahead, then the extra one
+    if constexpr (PRO > 0) {
+        // the ring's first block, refilled past the extra blocks, then those
         read_a(fr[0], kb_begin);
         compute(fr[0], kb_begin);
         __builtin_amdgcn_sched_barrier(0);
-        load(fr[0], kb_begin + 2);
+        load(fr[0], kb_begin + 1 + PRO);
         __builtin_amdgcn_sched_barrier(0);
-        read_a(fx, kb_begin + 1);
-        compute(fx, kb_begin + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        kb_loop = kb_begin + 2;
+#pragma unroll
+        for (int x = 0; x < PRO; ++x) {
+            read_a(fx[x], kb_begin + 1 + x);
+            compute(fx[x], kb_begin + 1 + x);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        kb_loop = kb_begin + 1 + PRO;
     }
     for (int kb0 = kb_loop; kb0 < kb_end; kb0 += PF * UNROLL) {
 #pragma unroll
