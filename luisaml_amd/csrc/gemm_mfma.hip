@@ -137,10 +137,14 @@ struct GemmArgs {
     uint32_t a_bytes, b_bytes;  // buffer extents for range checking
     int tiles_m, tiles_n;
     int nk;           // K steps of 128
-    // row slices (the conv's 2x4 layout on a grid of one tile column): tiles
-    // 0 .. slice_first-1 are whole BM-row tiles, the ones after them
-    // slice_rows rows each (a multiple of 32, below BM); 0: no slices
-    int slice_first, slice_rows;
+    // row slices of the 2x4 layout (slice_rows: 0 for none, else a multiple
+    // of 32 below BM).  slice_cols == 0 (a grid of one tile column): ids
+    // 0 .. slice_first-1 are whole BM-row tiles, the ids after them slices of
+    // slice_rows rows below those.  slice_cols > 0: the first slice_first =
+    // slice_cols * tiles_m ids are the whole tiles of the first slice_cols
+    // tile columns, the ids after them slices of slice_rows rows of the
+    // other columns, ceil(M / slice_rows) per column.
+    int slice_first, slice_rows, slice_cols;
     Epilogue e;
 };
 
@@ -177,19 +181,23 @@ __device__ inline int a_lds_off(int r, int c) { return r * BK + ((c ^ a_swz(r)) 
 // software rounding) took ~19 us for a 256x256 tile's bf16 epilogue, this one
 // ~4.5 us (fp32: ~8 us); on the 4096-row transformer linears that is 6-7% of
 // the exact kernel's time and 15-18% of the native FP8 one's.
+// Rows from rows_end on (M, or the end of the wavefront's rows in a row
+// slice, whose rows after it are another slice's) are dropped as rows past M
+// are: the buffer's extent ends there.
 // AMAX: m accumulates max |value| over the in-range elements written (rows
-// below M, columns below N; NaN compares false and is skipped).
+// below rows_end, columns below N; NaN compares false and is skipped).
 template <int ACT, bool HAS_C, bool BF16, bool AMAX = false>
 __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, int64_t row0, int64_t col, bool cols_ok,
-                                         float sc0, float sc1, float cb0, float cb1, float &m, bool c1_ok) {
+                                         float sc0, float sc1, float cb0, float cb1, float &m, bool c1_ok,
+                                         int64_t rows_end) {
     // every operation rounds on its own, as in epi_value_cv (where alpha is
     // applied under a runtime test, so nothing fuses across it): no FMA
 #pragma clang fp contract(off)
     constexpr uint32_t ES = BF16 ? 2 : 4;
     const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(e.y, 0, (int)(e.M * e.ldy * ES), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(e.y, 0, (int)(rows_end * e.ldy * ES), 0x00020000);
     const uint32_t step = (uint32_t)(2 * e.ldy * ES);
-    uint32_t off = cols_ok && row0 < e.M ? (uint32_t)((row0 * e.ldy + col) * ES) : OOB;
+    uint32_t off = cols_ok && row0 < rows_end ? (uint32_t)((row0 * e.ldy + col) * ES) : OOB;
     const float alpha = e.alpha;
 #pragma unroll 8
     for (int q = 0; q < 32; ++q, off += step) {
@@ -202,7 +210,7 @@ __device__ __forceinline__ void epi_rows(const Epilogue &e, const float *src, in
         v0 = apply_act(v0, ACT);
         v1 = apply_act(v1, ACT);
         if constexpr (AMAX) {
-            const bool r_ok = row0 + 2 * q < e.M;
+            const bool r_ok = row0 + 2 * q < rows_end;
             const float a0 = fabsf(v0), a1 = fabsf(v1);
             m = r_ok && cols_ok && a0 > m ? a0 : m;
             m = r_ok && c1_ok && a1 > m ? a1 : m;
@@ -480,15 +488,19 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     // multiple of 8 whenever it is below the tile count, so every id of one
     // workgroup stays on its XCD's range).
     const int ntiles = g.tiles_m * g.tiles_n;
-    auto tile_origin = [&](int t, int64_t &om0, int64_t &on0) {
-        if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
-        const int per_group = GROUP_M * g.tiles_n;
+    // (over a grid of tm x tn tiles: the whole grid, or the whole-tile
+    // columns of a sliced one)
+    auto tile_origin_in = [&](int t, int tm, int tn, int64_t &om0, int64_t &on0) {
+        const int nt = tm * tn;
+        if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+        const int per_group = GROUP_M * tn;
         const int group = t / per_group;
         const int first_m = group * GROUP_M;
-        const int gsize = min(g.tiles_m - first_m, GROUP_M);
+        const int gsize = min(tm - first_m, GROUP_M);
         om0 = (int64_t)(first_m + (t % per_group) % gsize) * T::BM;
         on0 = (int64_t)((t % per_group) / gsize) * T::BN;
     };
+    auto tile_origin = [&](int t, int64_t &om0, int64_t &on0) { tile_origin_in(t, g.tiles_m, g.tiles_n, om0, on0); };
     int64_t m0, n0;
     tile_origin(blockIdx.x, m0, n0);
     // Row slices (SLICE, when the launcher sets them): workgroup t below
@@ -498,20 +510,29 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
     // ceil(L/2) blocks and wave row 1 the rest (4 and 4 in a whole tile), so
     // the two wavefronts that share a SIMD split a slice's blocks evenly;
     // each wavefront's loop runs MFMAs for its own blocks only.
-    constexpr bool SLICE = CONV && WAVES_M == 2 && WM == 4 && !T::ONE_PER_SIMD;
+    constexpr bool SLICE = WAVES_M == 2 && WM == 4 && !T::ONE_PER_SIMD;
     int tile_rows = T::BM;
     if constexpr (SLICE)
         if (g.slice_rows) {
             // within each part, ids regrouped so that each XCD (id % 8)
-            // takes one contiguous range of rows, as tile_origin does
-            // (slice_first is a multiple of 8, so id % 8 = part id % 8)
+            // takes one contiguous range, as tile_origin does (with
+            // slice_first a multiple of 8, id % 8 = part id % 8)
             const int t = (int)blockIdx.x, first = g.slice_first;
             const bool whole = t < first;
             const int s = whole ? t : t - first, cnt = whole ? first : (int)gridDim.x - first;
             const int q = cnt >> 3, r = cnt & 7, x = s & 7;
             const int idx = x * q + (x < r ? x : r) + (s >> 3);
-            m0 = whole ? (int64_t)idx * T::BM : (int64_t)first * T::BM + (int64_t)idx * g.slice_rows;
-            n0 = 0;
+            // (the conv slices one tile column only)
+            if (CONV || g.slice_cols == 0) {  // one tile column: whole row tiles, then slices below them
+                m0 = whole ? (int64_t)idx * T::BM : (int64_t)first * T::BM + (int64_t)idx * g.slice_rows;
+                n0 = 0;
+            } else if (whole) {  // the whole-tile columns, walked as an unsliced grid of them
+                tile_origin_in(t, g.tiles_m, g.slice_cols, m0, n0);
+            } else {  // the other columns, each cut into slices
+                const int spc = (int)((g.M + g.slice_rows - 1) / g.slice_rows);
+                m0 = (int64_t)(idx % spc) * g.slice_rows;
+                n0 = (int64_t)(g.slice_cols + idx / spc) * T::BN;
+            }
             tile_rows = whole ? T::BM : g.slice_rows;
         }
     const int live0 = (tile_rows / 32 + 1) / 2;  // 32-row blocks of wave row 0 (WM in a whole tile)
@@ -564,7 +585,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             a_iw0[i] = (int)ow * cv.sw - cv.pw;
         } else {
             // 32-bit: the host keeps (M - 1) * lda + K below 2^31
-            const bool in = (int)m0 + r < (int)g.M;
+            const bool in = r < tile_rows && (int)m0 + r < (int)g.M;
             a_off[i] = valid && in ? ((uint32_t)m0 + (uint32_t)r) * (uint32_t)g.lda + (uint32_t)(c * 16) : OOB;
             a_klim[i] = in ? (uint32_t)g.K : 0u;
         }
@@ -1300,6 +1321,10 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         static_assert(WN % 2 == 0 && WM % 2 == 0, "32-column and 32-row block pairs");
         constexpr int ER = T::EP_ROWS;
         float amax_m = 0.0f;  // AMAX: this lane's max |y|
+        // the end of this wavefront's rows: M, or in a row slice the end of
+        // its live blocks (the slice's later rows are another slice's)
+        const int64_t wend = m0 + wrow0 + (int64_t)wlive * 32;
+        const int64_t m_end = wend < e.M ? wend : e.M;
         float *st = reinterpret_cast<float *>(smem) + wave * (ER * EP2_PITCH);
 #pragma unroll
         for (int jp = 0; jp < WN / 2; ++jp) {
@@ -1326,7 +1351,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         auto fast_pass = [&](const float *src, int64_t row0) {
             auto go = [&](auto act, auto has_c, auto bf) {
                 epi_rows<decltype(act)::value, decltype(has_c)::value, decltype(bf)::value, AMAX>(
-                    e, src, row0, col, c0ok, sc0, sc1, cb0, cb1, amax_m, c1ok);
+                    e, src, row0, col, c0ok, sc0, sc1, cb0, cb1, amax_m, c1ok, m_end);
             };
             auto by_out = [&](auto act, auto has_c) {
                 if (e.y_bf16)
@@ -1360,7 +1385,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
             __syncthreads();
 #pragma unroll
             for (int sub = 0; sub < ER / 64; ++sub) {
-                const int64_t row0 = m0 + wm * WM * 32 + h * ER + sub * 64 + (lane >> 5);
+                const int64_t row0 = m0 + wrow0 + h * ER + sub * 64 + (lane >> 5);
                 const float *src = st + (sub * 64 + (lane >> 5)) * EP2_PITCH + 2 * (lane & 31);
                 if (fast) {
                     fast_pass(src, row0);
@@ -1371,7 +1396,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                             const int64_t row = row0 + 2 * q;
                             const float2 a = *reinterpret_cast<const float2 *>(src + 2 * q * EP2_PITCH);
                             const float v0 = epi_value_cv(e, sc0, cv0, a.x), v1 = epi_value_cv(e, sc1, cv1, a.y);
-                            if (row < e.M) {
+                            if (row < m_end) {
                                 if constexpr (AMAX) {
                                     amax_m = fabsf(v0) > amax_m ? fabsf(v0) : amax_m;
                                     amax_m = c1ok && fabsf(v1) > amax_m ? fabsf(v1) : amax_m;
@@ -1388,7 +1413,7 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
 #pragma unroll 1
                         for (int q = 0; q < 32; ++q) {
                             const int64_t row = row0 + 2 * q;
-                            if (row >= e.M) break;
+                            if (row >= m_end) break;
                             const float2 a = *reinterpret_cast<const float2 *>(src + 2 * q * EP2_PITCH);
                             const float v0 = epi_value(e, sc0, row, col, a.x);
                             if constexpr (AMAX) amax_m = fabsf(v0) > amax_m ? fabsf(v0) : amax_m;
@@ -1465,6 +1490,49 @@ int device_cus() {
 #ifndef LCML_CONV_SLICES
 #define LCML_CONV_SLICES 1
 #endif
+#ifndef LCML_GEMM_SLICES
+#define LCML_GEMM_SLICES 1
+#endif
+
+// Row slices of the 2x4 layout's last round of tiles (one workgroup per
+// CU): h = the rows left over the CUs, rounded up to 32 (at least 64, and
+// up again while the slices outnumber the CUs); none where h reaches BM.
+// One tile column (cols = 0): the last round's rows below the whole tiles,
+// e.g. 100352 rows (32 images of 56x56) as 256 whole tiles, then 218 slices
+// of 160 rows, instead of 392 whole tiles in two full rounds.  More
+// columns: the whole tiles of the first `cols` tile columns, then each
+// other column cut into slices, e.g. 4096x11008 as 512 whole tiles (32
+// columns), then 11 x 22 slices of 192 rows, instead of 688 whole tiles in
+// 2.69 rounds.
+struct SlicePlan {
+    int first = 0, rows = 0, cols = 0;
+    int64_t grid = 0;
+};
+SlicePlan plan_slices(int64_t M, int tiles_m, int tiles_n, int BM, int64_t cus) {
+    SlicePlan p;
+    p.grid = (int64_t)tiles_m * tiles_n;
+    const int64_t round0 = (p.grid - 1) / cus * cus;  // whole tiles before the last round
+    int64_t first, rem, cols = 0;
+    if (tiles_n == 1) {
+        first = round0;
+        rem = M - first * BM;
+    } else {
+        cols = round0 / tiles_m;  // whole tile columns
+        if (cols < 1) return p;
+        first = cols * tiles_m;
+        rem = (tiles_n - cols) * M;
+    }
+    int64_t h = ((rem + cus - 1) / cus + 31) / 32 * 32;
+    h = h < 64 ? 64 : h;
+    auto slices = [&](int64_t hh) { return tiles_n == 1 ? (rem + hh - 1) / hh : (tiles_n - cols) * ((M + hh - 1) / hh); };
+    while (h < BM && slices(h) > cus) h += 32;
+    if (h >= BM) return p;
+    p.first = (int)first;
+    p.rows = (int)h;
+    p.cols = (int)cols;
+    p.grid = first + slices(h);
+    return p;
+}
 
 template <class Cfg, int WMv, int WNv, int WMb, int WNb, bool EXACT, bool CONV, bool PP = false, bool DIRECT = false,
           bool AMAX = false>
@@ -1488,25 +1556,16 @@ hipError_t launch_cfg(GemmArgs &g, hipStream_t s) {
     // more), each walking tiles blockIdx.x + k * gridDim.x
     int grid = g.tiles_m * g.tiles_n;
     if constexpr (DIRECT) grid = grid < device_cus() ? grid : device_cus();
-    // The conv on the 2x4 layout, one tile column, no groups: the last round
-    // of whole tiles (one workgroup per CU) becomes slices of h rows, h the
-    // rows left over the CUs rounded up to 32 (at least 64), so that every
-    // CU takes a share of it: 100352 rows (32 images of 56x56) run as 256
-    // whole tiles, then 218 slices of 160 rows, instead of 392 whole tiles
-    // (two full rounds).
-    g.slice_first = g.slice_rows = 0;
-    if constexpr (CONV && WMv == 2 && WMb == 4 && !Cfg::ONE_PER_SIMD)
-        if (LCML_CONV_SLICES && g.tiles_n == 1 && g.cv.CoutTot == (int)g.N) {
-            const int64_t cus = device_cus();
-            const int64_t first = (int64_t)(g.tiles_m - 1) / cus * cus;  // whole tiles before the last round
-            const int64_t rem = g.M - first * Cfg::BM;                    // rows of the last round (> 0)
-            int64_t h = ((rem + cus - 1) / cus + 31) / 32 * 32;
-            h = h < 64 ? 64 : h;
-            if (h < Cfg::BM) {
-                g.slice_first = (int)first;
-                g.slice_rows = (int)h;
-                grid = (int)(first + (rem + h - 1) / h);
-            }
+    // the 2x4 layout's last round as row slices (plan_slices): the conv on
+    // one tile column without groups, and the GEMM
+    g.slice_first = g.slice_rows = g.slice_cols = 0;
+    if constexpr (WMv == 2 && WMb == 4 && !Cfg::ONE_PER_SIMD)
+        if (CONV ? LCML_CONV_SLICES && g.tiles_n == 1 && g.cv.CoutTot == (int)g.N : LCML_GEMM_SLICES) {
+            const SlicePlan p = plan_slices(g.M, g.tiles_m, g.tiles_n, Cfg::BM, device_cus());
+            g.slice_first = p.first;
+            g.slice_rows = p.rows;
+            g.slice_cols = p.cols;
+            grid = (int)p.grid;
         }
     hipLaunchKernelGGL((k_gemm_mfma<WMv, WNv, WMb, WNb, EXACT, CONV, PP, DIRECT, AMAX>),
                        dim3(grid, CONV ? g.cv.CoutTot / (int)g.N : 1), dim3(Cfg::NT), Cfg::LDS_BYTES, s, g);
@@ -1577,7 +1636,11 @@ hipError_t launch_gemm_mfma(int64_t M, int64_t N, int64_t K, const uint8_t *a, i
 
 int64_t gemm_mfma_workgroups(int64_t M, int64_t N, bool small_tiles) {
     const int64_t t = small_tiles ? 128 : 256;
-    return ((M + t - 1) / t) * ((N + t - 1) / t);
+    const int tm = (int)((M + t - 1) / t), tn = (int)((N + t - 1) / t);
+    // the amax-partials launch (an fp32 output) on 256x256 tiles takes the
+    // 2x4 layout, whose last round may run as row slices
+    if (!small_tiles && LCML_GEMM_SLICES) return plan_slices(M, tm, tn, Shipped::BM, device_cus()).grid;
+    return (int64_t)tm * tn;
 }
 
 hipError_t launch_conv_mfma(const uint8_t *x_nhwc, int64_t Nb, int C, int H, int W, const uint8_t *bp, int Cout,
