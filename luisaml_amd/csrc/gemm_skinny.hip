@@ -25,17 +25,19 @@
 //
 // DYN (fused DynamicQuantizeLinear): the activations arrive as fp32 and are
 // quantised inside the kernel.  Every workgroup first starts the loads of
-// the first weight K block of each wavefront, then reduces amax = max|x|
-// over the whole activation matrix (L2-resident: all workgroups read the same M*K floats),
-// derives the per-tensor scale amax/448 exactly as the standalone dynamic
-// quantiser does, and encodes the rows into LDS (row pitch Kp+16 bytes, so
-// the 16 rows of a fragment read fall in distinct banks; k >= K is zero).
-// The main loop then reads the activation operand from LDS.  The redundant
-// per-workgroup amax and encode cost M*K loads and ~20 VALU operations per
-// element in every workgroup (measured on the 4096x11008 linear: +2.2 us at
-// M=1, +2.8 us at M=2, +5 us at M=4 over the GEMM alone, against about
-// +4.5 us for the separate quantise launch), so the fused kernel only pays
-// off for small M*K.
+// the first two weight K blocks of each wavefront, then reduces amax =
+// max|x| over the whole activation matrix (L2-resident: all workgroups read
+// the same M*K floats) and derives the per-tensor scale amax/448 exactly as
+// the standalone dynamic quantiser does.  Each wavefront then encodes the
+// activations of its own K blocks into LDS (row pitch Kp+16 bytes, so the 16
+// rows of a fragment read fall in distinct banks; k >= K is zero), one block
+// at a time, right after issuing that block's weight loads: the ~40 VALU
+// operations per float4 of the exact encode run while the weights are in
+// flight, and only the first block's encode delays the stream (encoding all
+// of x before the main loop cost 1.55 us at M=1 and 2.6 us at M=4 over the
+// E4M3-in kernel on the 4096x11008 linear; per block, 1.4 and 1.7 us).  The
+// redundant per-workgroup amax and encode still cost M*K loads and VALU work
+// in every workgroup, so the fused kernel only pays off for small M*K.
 #include <algorithm>
 
 #include "lcml_internal.hpp"
@@ -54,9 +56,6 @@ namespace {
 #endif
 #ifndef LCML_SKINNY_PF
 #define LCML_SKINNY_PF 1
-#endif
-#ifndef LCML_SKINNY_PRO
-#define LCML_SKINNY_PRO 1
 #endif
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every extent: loads return zeros
@@ -91,9 +90,13 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN>
+// SB (DYN only): activation slots of 4 floats per lane per K block, at least
+// ceil(M/2)
+template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     static_assert(!DYN || MB == 1, "the fused quantiser serves M <= 16");
+    static_assert(!DYN || (SB >= 1 && SB <= 8 && LCML_SKINNY_PF == 1 && UNROLL == 1),
+                  "the fused quantiser: M <= 2*SB <= 16, one K block per load");
     constexpr int NT = WAVES * 64;
     __shared__ v4f red[WAVES][NB][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // DYN: [M][pitch] E4M3
@@ -105,17 +108,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // ids go round-robin over the 8 XCDs (id % 8), so ids are regrouped into
     // one contiguous range per XCD, in which the row groups of a panel are
     // consecutive.
-    int64_t t = blockIdx.x;
-    if (g.rg > 1) {
-        const int64_t nwg = (int64_t)gridDim.x, q = nwg >> 3, r = nwg & 7, x = t & 7;
-        t = x * q + (x < r ? x : r) + (t >> 3);
+    // Every instruction before the first weight load delays the whole
+    // stream: with MB = 1 (M <= 16) there is one row group, so the mapping
+    // needs no division (a 64-bit one costs ~200 instructions, 0.1-0.25 us
+    // per launch on the 4096x11008 linear).
+    int64_t blk0, row0;  // first 16-column block, first row
+    if constexpr (MB == 1) {
+        blk0 = (int64_t)blockIdx.x * NB;
+        row0 = 0;
+    } else {
+        int64_t t = blockIdx.x;
+        if (g.rg > 1) {
+            const int64_t nwg = (int64_t)gridDim.x, q = nwg >> 3, r = nwg & 7, x = t & 7;
+            t = x * q + (x < r ? x : r) + (t >> 3);
+        }
+        blk0 = (t / g.rg) * NB;
+        row0 = (t - (t / g.rg) * g.rg) * 16 * MB;
     }
-    const int64_t blk0 = (t / g.rg) * NB;                   // first 16-column block
-    const int64_t row0 = (t - (t / g.rg) * g.rg) * 16 * MB;  // first row
 
-    // K range of this wavefront
-    const int kb_begin = (int)(((int64_t)g.nkb * wave) / WAVES);
-    const int kb_end = (int)(((int64_t)g.nkb * (wave + 1)) / WAVES);
+    // K range of this wavefront (nkb < 2^24)
+    const int kb_begin = (g.nkb * wave) / WAVES;
+    const int kb_end = (g.nkb * (wave + 1)) / WAVES;
 
     // Every global load below is a buffer load whose out-of-range lanes and
     // blocks carry an offset past the buffer's extent: the hardware returns
@@ -272,10 +285,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         const uint32_t o = i < nq ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
         return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
     };
+    // DYN: the activations of one K block for the per-block encode: lane l,
+    // slot s holds row 2s + l/32, float4 column l%32 of the block (rows past
+    // M and columns past K load zeros)
+    f4 xb0[DYN ? SB : 1], xb1[DYN ? SB : 1];
+    auto xload_block = [&](f4 *xb, int kb) {
+        const bool in = kb < kb_end;
+#pragma unroll
+        for (int sl = 0; sl < SB; ++sl) {
+            const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
+            const bool ok = in & (r < (uint32_t)g.M) & (c < kq);
+            const uint32_t o = ok ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
+            xb[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
+        }
+    };
     f4 v[UQ];
     if constexpr (DYN) {
 #pragma unroll
         for (int u = 0; u < UQ; ++u) v[u] = xq(u * NT + tid);
+        xload_block(xb0, kb_begin);
+        xload_block(xb1, kb_begin + 1);
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -283,17 +312,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         load(fr[p], kb_begin + p * UNROLL);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // DYN: PRO more K blocks in flight while the activations are quantised
-    // (consumed right after the quantisation; the ring itself stays PF deep)
-    constexpr int PRO = DYN ? LCML_SKINNY_PRO : 0;
-    static_assert(PRO == 0 || (PF == 1 && UNROLL == 1), "the extra blocks follow the ring's first");
-    Frag fx[PRO > 0 ? PRO : 1];
-#pragma unroll
-    for (int x = 0; x < PRO; ++x) {
-        load(fx[x], kb_begin + 1 + x);
+    // DYN: a second K block in flight while the scale is computed
+    Frag fx;
+    if constexpr (DYN) {
+        load(fx, kb_begin + 1);
         __builtin_amdgcn_sched_barrier(0);
     }
     float a_dyn = 1.0f;
+    Recip d{1.0f, 1.0f, true};
+    int enc_mode = 2;
     if constexpr (DYN) {
         __shared__ float wmax[WAVES];
         __shared__ uint32_t wbad[WAVES];
@@ -333,81 +360,78 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         }
         a_dyn = scale_from_amax_bits(f32_bits(m));
         if (g.scale_out && blockIdx.x == 0 && tid == 0) *g.scale_out = a_dyn;
-        const Recip d = make_recip(a_dyn);
-        // the scale's range test and the NaN/inf test are uniform: one
-        // branch outside the loops (mode 2: fast scale and clean input, 1:
-        // fast scale, 0: IEEE division)
-        auto encode_all = [&](auto mode) {
-            auto put = [&](uint32_t i, f4 x4) {
-                uint32_t r, c;
-                split(i, r, c);
-                uint32_t code;
-                if constexpr (decltype(mode)::value == 2)
-                    code = quantize4_clean(x4.x, x4.y, x4.z, x4.w, d);
-                else
-                    code = quantize4_t<decltype(mode)::value == 1>(x4.x, x4.y, x4.z, x4.w, d);
-                reinterpret_cast<uint32_t *>(a_lds + r * pitch)[c] = code;
-            };
-            if (nq <= NT * UQ) {  // one round: the values are still in registers
+        d = make_recip(a_dyn);
+        // the scale's range test and the NaN/inf test are uniform (mode 2:
+        // fast scale and clean input, 1: fast scale, 0: IEEE division)
+        enc_mode = d.fast ? (bad ? 1 : 2) : 0;
+    }
+    // DYN: block kb's codes into this wavefront's own columns of the LDS
+    // copy (rows below M; columns past K get the zeros x holds there).  Only
+    // this wavefront reads them, and a wavefront's LDS accesses take effect
+    // in order, so no barrier is needed.
+    auto encode_block = [&](const f4 *xb, int kb) {
+        if (kb >= kb_end) return;
+        auto run = [&](auto mode) {
 #pragma unroll
-                for (int u = 0; u < UQ; ++u) {
-                    const uint32_t i = u * NT + tid;
-                    if (i < nq) put(i, v[u]);
-                }
-            } else {
-                for (uint32_t base = 0; base < nq; base += NT * UQ) {
-#pragma unroll
-                    for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
-#pragma unroll
-                    for (int u = 0; u < UQ; ++u) {
-                        const uint32_t i = base + u * NT + tid;
-                        if (i < nq) put(i, v[u]);
-                    }
+            for (int sl = 0; sl < SB; ++sl) {
+                const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
+                if (r < (uint32_t)g.M) {
+                    const f4 x4 = xb[sl];
+                    uint32_t code;
+                    if constexpr (decltype(mode)::value == 2)
+                        code = quantize4_clean(x4.x, x4.y, x4.z, x4.w, d);
+                    else
+                        code = quantize4_t<decltype(mode)::value == 1>(x4.x, x4.y, x4.z, x4.w, d);
+                    reinterpret_cast<uint32_t *>(a_lds + r * pitch)[c] = code;
                 }
             }
         };
-        if (d.fast && !bad)
-            encode_all(std::integral_constant<int, 2>{});
-        else if (d.fast)
-            encode_all(std::integral_constant<int, 1>{});
+        if (enc_mode == 2)
+            run(std::integral_constant<int, 2>{});
+        else if (enc_mode == 1)
+            run(std::integral_constant<int, 1>{});
         else
-            encode_all(std::integral_constant<int, 0>{});
-        const uint32_t zq = (uint32_t)(pitch - 16) / 4 - kq;  // zero words per row for K <= k < Kp
-        for (uint32_t i = tid; i < (uint32_t)g.M * zq; i += NT) {
-            const uint32_t r = i / zq;
-            reinterpret_cast<uint32_t *>(a_lds + r * pitch)[kq + (i - r * zq)] = 0u;
-        }
-        __syncthreads();
-    }
-    // consume buffer p (blocks kb), refill it with the blocks PF*UNROLL ahead
-    // (past the end: zeros, no memory traffic).  The scheduling barriers keep
-    // each buffer's loads together and in ring order, so the wait before a
-    // buffer's first use leaves the other PF-1 buffers' loads in flight.
-    int kb_loop = kb_begin;
-    if constexpr (PRO > 0) {
-        // the ring's first block, refilled past the extra blocks, then those
+            run(std::integral_constant<int, 0>{});
+    };
+    if constexpr (DYN) {
+        // blocks 0 and 1 are in flight; each later block's activations are
+        // loaded with its weights and encoded while those are in flight
+        encode_block(xb0, kb_begin);
         read_a(fr[0], kb_begin);
         compute(fr[0], kb_begin);
         __builtin_amdgcn_sched_barrier(0);
-        load(fr[0], kb_begin + 1 + PRO);
+        xload_block(xb0, kb_begin + 2);
+        load(fr[0], kb_begin + 2);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int x = 0; x < PRO; ++x) {
-            read_a(fx[x], kb_begin + 1 + x);
-            compute(fx[x], kb_begin + 1 + x);
+        encode_block(xb1, kb_begin + 1);
+        read_a(fx, kb_begin + 1);
+        compute(fx, kb_begin + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        encode_block(xb0, kb_begin + 2);
+        for (int kb = kb_begin + 2; kb < kb_end; ++kb) {
+            read_a(fr[0], kb);
+            compute(fr[0], kb);
             __builtin_amdgcn_sched_barrier(0);
+            xload_block(xb0, kb + 1);
+            load(fr[0], kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            encode_block(xb0, kb + 1);
         }
-        kb_loop = kb_begin + 1 + PRO;
-    }
-    for (int kb0 = kb_loop; kb0 < kb_end; kb0 += PF * UNROLL) {
+    } else {
+        // consume buffer p (blocks kb), refill it with the blocks PF*UNROLL
+        // ahead (past the end: zeros, no memory traffic).  The scheduling
+        // barriers keep each buffer's loads together and in ring order, so
+        // the wait before a buffer's first use leaves the other PF-1
+        // buffers' loads in flight.
+        for (int kb0 = kb_begin; kb0 < kb_end; kb0 += PF * UNROLL) {
 #pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const int kb = kb0 + p * UNROLL;
-            if constexpr (DYN) read_a(fr[p], kb);
-            compute(fr[p], kb);
-            __builtin_amdgcn_sched_barrier(0);
-            load(fr[p], kb + PF * UNROLL);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int p = 0; p < PF; ++p) {
+                const int kb = kb0 + p * UNROLL;
+                compute(fr[p], kb);
+                __builtin_amdgcn_sched_barrier(0);
+                load(fr[p], kb + PF * UNROLL);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 
@@ -518,15 +542,24 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
     const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
-    const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true>)
-                           : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true>);
-    static std::atomic<uint64_t> lds_set[2];
-    if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess) return err;
-    if (exact)
-        hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true>), dim3(grid), dim3(W * 64), lds, s, g);
-    else
-        hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true>), dim3(grid), dim3(W * 64), lds, s, g);
-    return hipGetLastError();
+    // activation slots per lane per K block: ceil(M/2), rounded up to 1, 2, 4, 8
+    auto run = [&](auto sb) -> hipError_t {
+        constexpr int SB = decltype(sb)::value;
+        const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true, SB>)
+                               : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true, SB>);
+        static std::atomic<uint64_t> lds_set[2];
+        if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess)
+            return err;
+        if (exact)
+            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true, SB>), dim3(grid), dim3(W * 64), lds, s, g);
+        else
+            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true, SB>), dim3(grid), dim3(W * 64), lds, s, g);
+        return hipGetLastError();
+    };
+    if (M <= 2) return run(std::integral_constant<int, 1>{});
+    if (M <= 4) return run(std::integral_constant<int, 2>{});
+    if (M <= 8) return run(std::integral_constant<int, 4>{});
+    return run(std::integral_constant<int, 8>{});
 }
 
 }  // namespace lcml
