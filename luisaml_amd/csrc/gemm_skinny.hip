@@ -312,6 +312,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         load(fr[p], kb_begin + p * UNROLL);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // MB = 1: the epilogue's weight scales (thread t writes outputs t + i*NT),
+    // read while the weight stream runs, as buffer loads outside any branch
+    // (a load under a branch would make the first K block's wait drain them
+    // too); a missing scale reads 0 and is replaced by 1
+    constexpr int EPO = (NB * 256 + NT - 1) / NT;
+    float bsc[EPO];
+    if constexpr (MB == 1) {
+        const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)g.e.b_scale, 0, g.e.b_scale ? (int)((g.e.b_per_channel ? g.e.N : 1) * 4) : 0, kRsrcFlags);
+#pragma unroll
+        for (int i = 0; i < EPO; ++i) {
+            const int o = tid + i * NT, j = o >> 8, l = o & 63;
+            const int64_t col = (blk0 + (j < NB ? j : 0)) * 16 + (l & 15);
+            const uint32_t so = g.e.b_per_channel ? (col < g.e.N ? (uint32_t)col * 4 : kOOB) : 0u;
+            bsc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (int)so, 0, 0));
+        }
+        if (!g.e.b_scale) {
+#pragma unroll
+            for (int i = 0; i < EPO; ++i) bsc[i] = 1.0f;
+        }
+    }
     // DYN: a second K block in flight while the scale is computed
     Frag fx;
     if constexpr (DYN) {
@@ -446,15 +467,30 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[mb][j];
         __syncthreads();
-        for (int o = tid; o < NB * 256; o += NT) {
-            const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
-            const int64_t row = row0 + mb * 16 + (l >> 4) * 4 + r;
-            const int64_t col = (blk0 + j) * 16 + (l & 15);
-            if (row >= e.M || col >= e.N) continue;
-            float v = 0.0f;
+        if constexpr (MB == 1) {
 #pragma unroll
-            for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
-            epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
+            for (int i = 0; i < EPO; ++i) {
+                const int o = tid + i * NT;
+                const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
+                const int64_t row = row0 + (l >> 4) * 4 + r;
+                const int64_t col = (blk0 + j) * 16 + (l & 15);
+                if (o >= NB * 256 || row >= e.M || col >= e.N) continue;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
+                epi_store(e, row, col, epi_value(e, a_s * bsc[i], row, col, v));
+            }
+        } else {
+            for (int o = tid; o < NB * 256; o += NT) {
+                const int j = o >> 8, l = o & 63, r = (o >> 6) & 3;
+                const int64_t row = row0 + mb * 16 + (l >> 4) * 4 + r;
+                const int64_t col = (blk0 + j) * 16 + (l & 15);
+                if (row >= e.M || col >= e.N) continue;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
+                epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
+            }
         }
     }
 }
