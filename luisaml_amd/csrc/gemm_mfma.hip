@@ -725,8 +725,8 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
         // gains) and on grids of one tile column it loses 3-6%; those keep
         // the 2x4 layout.
         constexpr int NF = WM + WN;
-        static_assert(NF == 8 && T::LOADS <= 14 && NSTAGE >= 4,
-                      "schedule: 16 chunk reads of 4+4 fragments, the loads on the MFMAs after the barrier");
+        static_assert(NF == 8 && T::LOADS == 8 && NSTAGE >= 4,
+                      "schedule: 16 chunk reads of 4+4 fragments, 8 loads spread over the MFMAs after the barrier");
         u4 f0[NF][2], f1[NF][2];  // raw E4M3 fragments [A0..A3, B0..B3][16-byte chunk]
         // The 16 chunk reads of a step, q = 0..15 in the order the first
         // MFMAs of a step use them: A0, B0..B3, A1..A3 (two chunks each).
@@ -876,13 +876,18 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                     if ((b & 1) == 0) conv(cv0, fc, 2, b >> 1);
                     if (!LAST && b < 2) read(fn, rst, 14 + b);
                     if (LAST && b == 2) load_coef(rso);
-                    if (b >= 2 && b < 2 + T::LOADS) load(lst, lt, b - 2, checked);
+                    // the 8 loads one per 4 MFMAs over substeps 1 and 2: in
+                    // a burst, the four wavefronts' loads fill the TA's
+                    // command FIFO and a stalled load holds up the MFMAs
+                    // issued after it (+0.7% at 8192^3)
+                    if ((b & 3) == 3) load(lst, lt, b >> 2, checked);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int b = 0; b < 16; ++b) {
                     mma(cv0, b, Acc{});
                     if ((b & 1) == 0) conv(cv1, fc, 3, b >> 1);
+                    if ((b & 3) == 3) load(lst, lt, 4 + (b >> 2), checked);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): fn landed
@@ -910,20 +915,22 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64, LCML_GEMM_WG_PER_CU) void k_
                 mma(0);
                 mma(1);
                 sync_step();
+                // the loads spread over all 14 MFMAs after the barrier (load
+                // l on the MFMA after ceil(14*l/8) - 1 of them): in a burst
+                // on the last six, the four wavefronts' loads fill the TA's
+                // command FIFO and a stalled load holds up the MFMAs issued
+                // after it (+1% at 8192^3)
                 int l = 0;
 #pragma unroll
                 for (int b = 2; b < 16; ++b) {
                     mma(b);
-                    if (b < 10) {
-                        if (!LAST) {
-                            read(fn, rst, 2 * (b - 2));
-                            read(fn, rst, 2 * (b - 2) + 1);
-                        }
-                    } else {
-                        if (LAST && b == 10) load_coef(rso);
-#pragma unroll
-                        for (int n = (T::LOADS - l + 15 - b) / (16 - b); n > 0; --n, ++l) load(lst, lt, l, checked);
+                    if (b < 10 && !LAST) {
+                        read(fn, rst, 2 * (b - 2));
+                        read(fn, rst, 2 * (b - 2) + 1);
                     }
+                    if (LAST && b == 2) load_coef(rso);
+#pragma unroll
+                    for (int n = ((b - 1) * T::LOADS + 13) / 14 - l; n > 0; --n, ++l) load(lst, lt, l, checked);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
