@@ -35,7 +35,7 @@
 // operations per float4 of the exact encode run while the weights are in
 // flight, and only the first block's encode delays the stream (encoding all
 // of x before the main loop cost 1.55 us at M=1 and 2.6 us at M=4 over the
-// E4M3-in kernel on the 4096x11008 linear; per block, 1.4 and 1.7 us).  The
+// E4M3-in kernel on the 4096x11008 linear; per block, 1.1 and 1.7 us).  The
 // redundant per-workgroup amax and encode still cost M*K loads and VALU work
 // in every workgroup, so the fused kernel only pays off for small M*K.
 #include <algorithm>
