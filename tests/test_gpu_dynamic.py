@@ -37,7 +37,9 @@ def two_step(x_d, bp, d_sw, N, K, kernel, **kw):
     return capi.gemm(q, s, bp, d_sw, N, K, kernel=kernel, **kw), q, s
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 7, 16])
+# every count of activation slots per lane (1, 2, 4, 8) and partly used
+# slots (odd M; rows past M in a slot's upper half-wave)
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 9, 13, 16])
 @pytest.mark.parametrize("N,K", [(11008, 4096), (320, 272), (100, 784), (4096, 5888)])
 @pytest.mark.parametrize("kernel", [capi.KERNEL_AUTO, capi.KERNEL_SKINNY, capi.KERNEL_SKINNY_FP8])
 def test_fused_matches_two_step_and_oracle(dev, M, N, K, kernel):
