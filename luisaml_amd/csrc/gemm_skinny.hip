@@ -91,8 +91,9 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // SB (DYN only): activation slots of 4 floats per lane per K block, at least
-// ceil(M/2)
-template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0>
+// ceil(M/2).  ONE (DYN only): every wavefront's K blocks fit 8 slots, so one
+// round of activation loads serves both the amax and the encode.
+template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0, bool ONE = false>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     static_assert(!DYN || MB == 1, "the fused quantiser serves M <= 16");
     static_assert(!DYN || (SB >= 1 && SB <= 8 && LCML_SKINNY_PF == 1 && UNROLL == 1),
@@ -300,7 +301,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         }
     };
     f4 v[UQ];
-    if constexpr (DYN) {
+    static_assert(!ONE || (DYN && UQ % SB == 0), "one round: whole blocks of slots");
+    if constexpr (ONE) {
+        // slot u holds slot u%SB of block kb_begin + u/SB (the per-block
+        // layout above): the amax reads these registers, and the encode
+        // takes them block by block, with no second load of x (-0.5 us at
+        // M=1, -0.75 us at M=4 on the 4096x11008 linear)
+#pragma unroll
+        for (int u = 0; u < UQ; ++u) {
+            const int kb = kb_begin + u / SB, sl = u % SB;
+            const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
+            const bool ok = (kb < kb_end) & (r < (uint32_t)g.M) & (c < kq);
+            const uint32_t o = ok ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
+            v[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (DYN) {
 #pragma unroll
         for (int u = 0; u < UQ; ++u) v[u] = xq(u * NT + tid);
         xload_block(xb0, kb_begin);
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         __shared__ uint32_t wbad[WAVES];
         float m = 0.0f;
         float nf = 0.0f;  // x * 0 summed: NaN once any x is NaN or +-inf
-        for (uint32_t base = 0; base < nq; base += NT * UQ) {
+        for (uint32_t base = 0; base < (ONE ? 1u : nq); base += NT * UQ) {
             if (base) {
 #pragma unroll
                 for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
@@ -414,7 +430,35 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         else
             run(std::integral_constant<int, 0>{});
     };
-    if constexpr (DYN) {
+    if constexpr (ONE) {
+        // the next block's activations are always v[0..SB-1]: after its
+        // encode the slots move down by SB
+        auto encode_v = [&](int kb) {
+            if (kb >= kb_end) return;
+            encode_block(v, kb);
+#pragma unroll
+            for (int u = 0; u + SB < UQ; ++u) v[u] = v[u + SB];
+        };
+        encode_v(kb_begin);
+        read_a(fr[0], kb_begin);
+        compute(fr[0], kb_begin);
+        __builtin_amdgcn_sched_barrier(0);
+        load(fr[0], kb_begin + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        encode_v(kb_begin + 1);
+        read_a(fx, kb_begin + 1);
+        compute(fx, kb_begin + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        encode_v(kb_begin + 2);
+        for (int kb = kb_begin + 2; kb < kb_end; ++kb) {
+            read_a(fr[0], kb);
+            compute(fr[0], kb);
+            __builtin_amdgcn_sched_barrier(0);
+            load(fr[0], kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            encode_v(kb + 1);
+        }
+    } else if constexpr (DYN) {
         // blocks 0 and 1 are in flight; each later block's activations are
         // loaded with its weights and encoded while those are in flight
         encode_block(xb0, kb_begin);
@@ -578,19 +622,27 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
     constexpr int NB = LCML_SKINNY_NB, W = LCML_SKINNY_WAVES, U = LCML_SKINNY_UNROLL;
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
     const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
-    // activation slots per lane per K block: ceil(M/2), rounded up to 1, 2, 4, 8
-    auto run = [&](auto sb) -> hipError_t {
+    // activation slots per lane per K block: ceil(M/2), rounded up to 1, 2,
+    // 4, 8; one round of activation loads when a wavefront's K blocks (at
+    // most ceil(nkb / W)) take at most 8 slots
+    auto run_one = [&](auto sb, auto one) -> hipError_t {
         constexpr int SB = decltype(sb)::value;
-        const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true, SB>)
-                               : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true, SB>);
+        constexpr bool ONE = decltype(one)::value;
+        const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true, SB, ONE>)
+                               : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true, SB, ONE>);
         static std::atomic<uint64_t> lds_set[2];
         if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess)
             return err;
         if (exact)
-            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true, SB>), dim3(grid), dim3(W * 64), lds, s, g);
+            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true, SB, ONE>), dim3(grid), dim3(W * 64), lds, s, g);
         else
-            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true, SB>), dim3(grid), dim3(W * 64), lds, s, g);
+            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true, SB, ONE>), dim3(grid), dim3(W * 64), lds, s,
+                               g);
         return hipGetLastError();
+    };
+    auto run = [&](auto sb) -> hipError_t {
+        if (((g.nkb + W - 1) / W) * decltype(sb)::value <= 8) return run_one(sb, std::true_type{});
+        return run_one(sb, std::false_type{});
     };
     if (M <= 2) return run(std::integral_constant<int, 1>{});
     if (M <= 4) return run(std::integral_constant<int, 2>{});
