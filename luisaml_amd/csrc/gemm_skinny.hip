@@ -33,11 +33,14 @@
 // rows of a fragment read fall in distinct banks; k >= K is zero), one block
 // at a time, right after issuing that block's weight loads: the ~40 VALU
 // operations per float4 of the exact encode run while the weights are in
-// flight, and only the first block's encode delays the stream (encoding all
-// of x before the main loop cost 1.55 us at M=1 and 2.6 us at M=4 over the
-// E4M3-in kernel on the 4096x11008 linear; per block, 1.1 and 1.7 us).  The
-// redundant per-workgroup amax and encode still cost M*K loads and VALU work
-// in every workgroup, so the fused kernel only pays off for small M*K.
+// flight, and only the first block's encode delays the stream.  When a
+// wavefront's blocks fit its 8 activation slots (ONE), the amax pass already
+// loads x in the per-block layout and the encode reuses those registers, so
+// x is read once.  (Encoding all of x before the main loop cost 1.55 us at
+// M=1 and 2.6 us at M=4 over the E4M3-in kernel on the 4096x11008 linear;
+// per block with one read of x, 0.6 and 1.0 us.)  The redundant
+// per-workgroup amax and encode still cost M*K loads and VALU work in every
+// workgroup, so the fused kernel only pays off for small M*K.
 #include <algorithm>
 
 #include "lcml_internal.hpp"
