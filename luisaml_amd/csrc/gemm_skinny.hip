@@ -381,10 +381,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
                 nf = fmaf(v[u].z, 0.0f, nf); nf = fmaf(v[u].w, 0.0f, nf);
             }
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float o = __shfl_xor(m, off, 64);
-            m = o > m ? o : m;
-        }
+        // by DPP within rows and readlane across them (on the critical path:
+        // a __shfl_xor ladder here cost 0.1-0.25 us per launch)
+        m = wave_max(m);
         const bool wave_bad = __builtin_amdgcn_ballot_w64(nf != nf) != 0;
         if (lane == 0) {
             wmax[wave] = m;

@@ -135,13 +135,21 @@ __device__ inline float scale_from_amax_bits(uint32_t bits) {
 }
 
 // max over a wavefront / a workgroup of THREADS threads (red: THREADS/64
-// floats of LDS); every thread gets the result
+// floats of LDS) of values m >= 0 (maxima of |x| with NaN skipped); every
+// thread gets the result.  For m >= 0 the max of the bit patterns is the max
+// of the values: within each 16-lane row by DPP shifts (lane 15 of a row ends
+// with the row's max; lanes shifted in from outside the row read 0), then the
+// four rows' lanes 15 by readlane.  A few VALU cycles, where a __shfl_xor
+// ladder is six LDS permute round trips.
 __device__ inline float wave_max(float m) {
-    for (int off = 32; off > 0; off >>= 1) {
-        float o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    return m;
+    int b = __builtin_bit_cast(int, m);
+    b = max(b, __builtin_amdgcn_update_dpp(0, b, 0x111, 0xf, 0xf, true));  // row_shr:1
+    b = max(b, __builtin_amdgcn_update_dpp(0, b, 0x112, 0xf, 0xf, true));  // row_shr:2
+    b = max(b, __builtin_amdgcn_update_dpp(0, b, 0x114, 0xf, 0xf, true));  // row_shr:4
+    b = max(b, __builtin_amdgcn_update_dpp(0, b, 0x118, 0xf, 0xf, true));  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(b, 15), r1 = __builtin_amdgcn_readlane(b, 31);
+    const int r2 = __builtin_amdgcn_readlane(b, 47), r3 = __builtin_amdgcn_readlane(b, 63);
+    return __builtin_bit_cast(float, max(max(r0, r1), max(r2, r3)));
 }
 
 template <int THREADS>
