@@ -152,6 +152,9 @@ __device__ inline float wave_max(float m) {
     return __builtin_bit_cast(float, max(max(r0, r1), max(r2, r3)));
 }
 
+// (wavefront 0 reduces the wavefront maxima and broadcasts the result through
+// red[0]: every thread reading all THREADS/64 of them after one barrier
+// measured 0.2 us slower in the small quantise launches)
 template <int THREADS>
 __device__ inline float block_max(float m, float *red) {
     m = wave_max(m);
