@@ -371,8 +371,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 #pragma unroll
                 for (int u = 0; u < UQ; ++u) v[u] = xq(base + u * NT + tid);
             }
+            // ONE: the slots past this wavefront's blocks hold zeros
+            const int nslot = ONE ? (kb_end - kb_begin) * SB : UQ;
 #pragma unroll
             for (int u = 0; u < UQ; ++u) {
+                if (u >= nslot) break;
                 // zeros past the end; NaN compares false and is skipped, as
                 // in the standalone amax
                 const float ax = fabsf(v[u].x), ay = fabsf(v[u].y), az = fabsf(v[u].z), aw = fabsf(v[u].w);

@@ -126,10 +126,23 @@ __device__ inline float div_fast(float x, const Recip &d) {
 
 __device__ inline float div_by(float x, const Recip &d) { return d.fast ? div_fast(x, d) : __fdiv_rn(x, d.s); }
 
+// a / 448 as div_fast's corrected product with r = RN(1/448): equal to the
+// IEEE quotient for every a in [2^-100, FLT_MAX], checked on all of them
+// (tests/test_oracle_codec.py, host build of this function)
+__host__ __device__ inline float div448_corrected(float a) {
+    constexpr float r = 1.0f / 448.0f;
+    const float q0 = a * r;
+    return fmaf(fmaf(-q0, 448.0f, a), r, q0);
+}
+
 // dynamic per-tensor scale from the fp32 bits of amax = max |x| over the
-// non-NaN elements: amax / 448, or 1 when that is not a positive finite number
+// non-NaN elements: amax / 448, or 1 when that is not a positive finite
+// number.  On the critical path of the dynamic quantisers, so the quotient
+// is div448_corrected where that is exact; zero, tiny amax and inf take the
+// division.
 __device__ inline float scale_from_amax_bits(uint32_t bits) {
-    float s = __fdiv_rn(bits_f32(bits), 448.0f);
+    const float a = bits_f32(bits);
+    float s = a >= 0x1p-100f && a <= 0x1.fffffep127f ? div448_corrected(a) : __fdiv_rn(a, 448.0f);
     if (!(s > 0.0f) || __builtin_isinf(s)) s = 1.0f;
     return s;
 }

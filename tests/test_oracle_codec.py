@@ -118,19 +118,39 @@ def test_quantize_dequantize_closed_forms():
     assert oracle.amax(np.array([1.0, np.nan, -5.0], np.float32)) == 5.0
 
 
-def test_product_encoder_matches_oracle_on_all_fp32(tmp_path):
-    """The HIP library's integer encoder (luisaml_amd/csrc/lcml_device.hpp,
-    compiled here for the host) against the oracle over all 2^32 patterns."""
+@pytest.fixture(scope="module")
+def host_lib(tmp_path_factory):
+    """luisaml_amd/csrc/lcml_device.hpp's host-callable functions, compiled
+    here for the host (tests/cpp/encoder_host.cpp)."""
     import ctypes
     import os
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     src = os.path.join(root, "tests", "cpp", "encoder_host.cpp")
-    so = str(tmp_path / "libenc_host.so")
+    so = str(tmp_path_factory.mktemp("host") / "libenc_host.so")
     subprocess.run(["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp",
                     "-I" + os.path.join(root, "luisaml_amd", "csrc"), src, "-o", so], check=True,
                    capture_output=True)
-    lib = ctypes.CDLL(so)
+    return ctypes.CDLL(so)
+
+
+def test_scale_quotient_matches_ieee_division_on_its_range(host_lib):
+    """The dynamic scale's amax / 448 (div448_corrected, the corrected
+    reciprocal product the device uses for amax in [2^-100, FLT_MAX]) equals
+    the IEEE quotient on every fp32 value of that range."""
+    import ctypes
+    host_lib.div448_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    host_lib.div448_mismatches.restype = ctypes.c_uint64
+    first, last = 0x0D800000, 0x7F800000  # 2^-100 .. FLT_MAX
+    assert np.float32(2.0 ** -100).view(np.uint32) == first
+    assert host_lib.div448_mismatches(first, last) == 0
+
+
+def test_product_encoder_matches_oracle_on_all_fp32(host_lib):
+    """The HIP library's integer encoder (luisaml_amd/csrc/lcml_device.hpp,
+    compiled here for the host) against the oracle over all 2^32 patterns."""
+    import ctypes
+    lib = host_lib
     lib.enc_range.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p]
     chunk = 1 << 28
     got = np.empty(chunk, np.uint8)
