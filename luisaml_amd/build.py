@@ -7,6 +7,9 @@ tree).  Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                             no v_pk_{add,mul,fma}_f32 generation
   -fvisibility=hidden                       only the LCML_API C symbols export
+  -mllvm -amdgpu-kernarg-preload-count=N    (gemm_skinny.hip, quantize.hip) the
+                                            N leading scalar kernel arguments
+                                            arrive in SGPRs at wave start
 Usage:  python -m luisaml_amd.build   (or luisaml_amd.build.build())
 """
 from __future__ import annotations
@@ -33,9 +36,20 @@ COMMON = [
 ]
 
 
+# per-file flags: leading scalar kernel arguments preloaded into SGPRs
+# instead of fetched by the first instructions (the small-M GEMM's first
+# weight loads depend on eight of them: 0.25-0.4 us per launch on the
+# 4096x11008 linear, with its shorter prologue; the quantisers' first loads
+# on four: 0.1 us)
+EXTRA = {
+    "gemm_skinny.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "quantize.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

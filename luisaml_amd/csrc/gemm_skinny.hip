@@ -91,14 +91,30 @@ __device__ inline v8i join(u4 lo, u4 hi) {
     return r;
 }
 
+// the kernel's leading scalar arguments, from the launch description g with
+// activations act of row stride ld (elements)
+#define LCML_SKINNY_LEAD(g, act, ld)                                                                               \
+    (g).bp, static_cast<const void *>(act), (int)(ld), (int)(g).M, (int)(g).K, (int)(g).KC, (g).nkb, (g).rg
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // SB (DYN only): activation slots of 4 floats per lane per K block, at least
 // ceil(M/2).  ONE (DYN only): every wavefront's K blocks fit 8 slots, so one
 // round of activation loads serves both the amax and the encode.
+// The values that the code before the first weight load reads come as
+// leading scalar arguments (bp, the activations a or x with their row
+// stride, M, K, the panel's k-chunks, the K blocks, the row groups), and
+// this file is compiled with -amdgpu-kernarg-preload-count=8: they arrive
+// in SGPRs when the wavefront starts, so the first loads wait for no
+// kernel-argument fetch.  The struct's copies of them are not read.  On the
+// 4096x11008 linear the preload alone saved 0.05-0.15 us per launch, and
+// with the 32-bit prologue below (one weight offset per lane, the blocks'
+// pieces as immediate offsets) 0.26-0.39 us.
 template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0, bool ONE = false>
-__global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
+__global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, const void *src, int ld, int M, int K,
+                                                            int kc, int nkb, int rg, SkinnyArgs g) {
     static_assert(!DYN || MB == 1, "the fused quantiser serves M <= 16");
+    static_assert(NB == 4, "a workgroup reads one whole 64-column panel");
     static_assert(!DYN || (SB >= 1 && SB <= 8 && LCML_SKINNY_PF == 1 && UNROLL == 1),
                   "the fused quantiser: M <= 2*SB <= 16, one K block per load");
     constexpr int NT = WAVES * 64;
@@ -116,23 +132,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // stream: with MB = 1 (M <= 16) there is one row group, so the mapping
     // needs no division (a 64-bit one costs ~200 instructions, 0.1-0.25 us
     // per launch on the 4096x11008 linear).
-    int64_t blk0, row0;  // first 16-column block, first row
+    int blk0, row0;  // first 16-column block, first row
     if constexpr (MB == 1) {
-        blk0 = (int64_t)blockIdx.x * NB;
+        blk0 = (int)blockIdx.x * NB;
         row0 = 0;
     } else {
-        int64_t t = blockIdx.x;
-        if (g.rg > 1) {
-            const int64_t nwg = (int64_t)gridDim.x, q = nwg >> 3, r = nwg & 7, x = t & 7;
+        int t = blockIdx.x;
+        if (rg > 1) {
+            const int nwg = (int)gridDim.x, q = nwg >> 3, r = nwg & 7, x = t & 7;
             t = x * q + (x < r ? x : r) + (t >> 3);
         }
-        blk0 = (t / g.rg) * NB;
-        row0 = (t - (t / g.rg) * g.rg) * 16 * MB;
+        blk0 = (t / rg) * NB;
+        row0 = (t - (t / rg) * rg) * 16 * MB;
     }
 
     // K range of this wavefront (nkb < 2^24)
-    const int kb_begin = (g.nkb * wave) / WAVES;
-    const int kb_end = (g.nkb * (wave + 1)) / WAVES;
+    const int kb_begin = (nkb * wave) / WAVES;
+    const int kb_end = (nkb * (wave + 1)) / WAVES;
 
     // Every global load below is a buffer load whose out-of-range lanes and
     // blocks carry an offset past the buffer's extent: the hardware returns
@@ -144,25 +160,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     const int arow = lane & 15;  // row within a 16-row block
     bool a_ok[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) a_ok[mb] = row0 + mb * 16 + arow < g.M;
+    for (int mb = 0; mb < MB; ++mb) a_ok[mb] = row0 + mb * 16 + arow < M;
 
-    // weights: this workgroup's 64-column panel (NB 16-column blocks)
-    const int64_t panel0 = blk0 >> 2;
+    // weights: this workgroup's 64-column panel (the grid covers the panels
+    // exactly, so its four 16-column blocks all exist).  Lane l reads column
+    // l%16 of each block and half l/16 of each k-chunk: block j's two
+    // 16-byte pieces of a K block lie at b_lane + j*256 and + 1024 from the
+    // K block's first byte.
     const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(g.bp + (panel0 < (g.nblk16 >> 2) ? panel0 : 0) * g.KC * 1024), 0, (int)(g.KC * 1024), kRsrcFlags);
-    uint32_t b_off[NB];
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int64_t blk = blk0 + j;
-        b_off[j] = blk < g.nblk16 ? (uint32_t)((((blk & 3) * 16 + (lane & 15)) * 16) + (lane >> 4) * 2 * 1024) : kOOB;
-    }
+        (void *)(bp + (size_t)(blk0 >> 2) * (size_t)kc * 1024), 0, kc * 1024, kRsrcFlags);
+    const uint32_t b_lane = (uint32_t)(lane & 15) * 16u + (uint32_t)(lane >> 4) * 2048u;
     // activations (E4M3, without DYN): row lane%16, k offset (lane/16)*32 of a K block
-    const __amdgpu_buffer_rsrc_t a_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void *)g.a, 0, DYN ? 0 : (int)((g.M - 1) * g.lda + g.K), kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        DYN ? nullptr : const_cast<void *>(src), 0, DYN ? 0 : (int)((int64_t)(M - 1) * ld + K), kRsrcFlags);
     uint32_t a_row_off[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
-        a_row_off[mb] = (uint32_t)((row0 + mb * 16 + arow) * g.lda) + (uint32_t)(lane >> 4) * 32;
+        a_row_off[mb] = (uint32_t)(row0 + mb * 16 + arow) * (uint32_t)ld + (uint32_t)(lane >> 4) * 32;
 
     v4f acc[MB][NB];
 #pragma unroll
@@ -178,11 +192,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         for (int u = 0; u < UNROLL; ++u) {
             const int kb = kb0 + u;
             const bool in = kb < kb_end;
+            // past the range: kOOB plus at most 1792, still past every extent
+            const uint32_t o = in ? b_lane + (uint32_t)kb * 8192u : kOOB;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                const uint32_t o = (in & (b_off[j] != kOOB)) ? b_off[j] + (uint32_t)kb * 8 * 1024 : kOOB;
-                f.blo[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)o, 0, kNT);
-                f.bhi[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)(o == kOOB ? kOOB : o + 1024), 0, kNT);
+                f.blo[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)(o + j * 256), 0, kNT);
+                f.bhi[u][j] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)(o + j * 256 + 1024), 0, kNT);
             }
             if constexpr (!DYN) {
                 const uint32_t k = (uint32_t)kb * 128 + (uint32_t)(lane >> 4) * 32;  // K < 2^31
@@ -190,8 +205,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
                 for (int mb = 0; mb < MB; ++mb) {
                     const uint32_t o = a_row_off[mb] + (uint32_t)kb * 128;
                     const bool ok = in & a_ok[mb];
-                    const uint32_t o_lo = (ok & (k < (uint32_t)g.K)) ? o : kOOB;
-                    const uint32_t o_hi = (ok & (k + 16 < (uint32_t)g.K)) ? o + 16 : kOOB;
+                    const uint32_t o_lo = (ok & (k < (uint32_t)K)) ? o : kOOB;
+                    const uint32_t o_hi = (ok & (k + 16 < (uint32_t)K)) ? o + 16 : kOOB;
                     f.alo[u][mb] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_lo, 0, 0);
                     f.ahi[u][mb] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)o_hi, 0, 0);
                 }
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         }
     };
     // DYN: activation fragments from the LDS copy (zero-padded to Kp)
-    const int64_t pitch = pad_to(g.K, kPackK) + 16;
+    const int64_t pitch = pad_to((int64_t)K, kPackK) + 16;
     auto read_a = [&](Frag &f, int kb0) {
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -269,10 +284,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     // of the weight prefetch so that it returns from L2 without queueing
     // behind the HBM loads.
     constexpr int UQ = 8;
-    const uint32_t kq = (uint32_t)(g.K / 4);
-    const uint32_t nq = (uint32_t)g.M * kq;
+    const uint32_t kq = (uint32_t)(K / 4);
+    const uint32_t nq = (uint32_t)M * kq;
     const __amdgpu_buffer_rsrc_t x_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void *)g.x, 0, DYN ? (int)(((g.M - 1) * g.ldx + g.K) * 4) : 0, kRsrcFlags);
+        __builtin_amdgcn_make_buffer_rsrc(DYN ? const_cast<void *>(src) : nullptr, 0,
+                                          DYN ? (int)(((int64_t)(M - 1) * ld + K) * 4) : 0, kRsrcFlags);
     // group i -> (row r, float4 c): i < 2^24, so the float quotient is off
     // by at most one and two compares fix it (no integer division)
     const float inv_kq = 1.0f / (float)kq;
@@ -286,7 +302,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
     auto xq = [&](uint32_t i) {
         uint32_t r, c;
         split(i, r, c);
-        const uint32_t o = i < nq ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
+        const uint32_t o = i < nq ? (r * (uint32_t)ld + c * 4) * 4 : kOOB;
         return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
     };
     // DYN: the activations of one K block for the per-block encode: lane l,
@@ -298,8 +314,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 #pragma unroll
         for (int sl = 0; sl < SB; ++sl) {
             const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
-            const bool ok = in & (r < (uint32_t)g.M) & (c < kq);
-            const uint32_t o = ok ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
+            const bool ok = in & (r < (uint32_t)M) & (c < kq);
+            const uint32_t o = ok ? (r * (uint32_t)ld + c * 4) * 4 : kOOB;
             xb[sl] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
         }
     };
@@ -314,8 +330,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
         for (int u = 0; u < UQ; ++u) {
             const int kb = kb_begin + u / SB, sl = u % SB;
             const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
-            const bool ok = (kb < kb_end) & (r < (uint32_t)g.M) & (c < kq);
-            const uint32_t o = ok ? (r * (uint32_t)g.ldx + c * 4) * 4 : kOOB;
+            const bool ok = (kb < kb_end) & (r < (uint32_t)M) & (c < kq);
+            const uint32_t o = ok ? (r * (uint32_t)ld + c * 4) * 4 : kOOB;
             v[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, (int)o, 0, 0));
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -417,7 +433,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(SkinnyArgs g) {
 #pragma unroll
             for (int sl = 0; sl < SB; ++sl) {
                 const uint32_t r = 2 * sl + (lane >> 5), c = (uint32_t)kb * 32 + (lane & 31);
-                if (r < (uint32_t)g.M) {
+                if (r < (uint32_t)M) {
                     const f4 x4 = xb[sl];
                     uint32_t code;
                     if constexpr (decltype(mode)::value == 2)
@@ -596,9 +612,11 @@ hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a,
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB * g.rg);
 #define LCML_SKINNY_LAUNCH(MBV)                                                                                  \
     if (exact)                                                                                                 \
-        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, true, false>), dim3(grid), dim3(W * 64), 0, s, g);     \
+        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, true, false>), dim3(grid), dim3(W * 64), 0, s,          \
+                           LCML_SKINNY_LEAD(g, g.a, g.lda), g);                                                 \
     else                                                                                                       \
-        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, false, false>), dim3(grid), dim3(W * 64), 0, s, g)
+        hipLaunchKernelGGL((k_gemm_skinny<NB, MBV, W, U, false, false>), dim3(grid), dim3(W * 64), 0, s,         \
+                           LCML_SKINNY_LEAD(g, g.a, g.lda), g)
     if (mb == 1) {
         LCML_SKINNY_LAUNCH(1);
     } else if (mb == 2) {
@@ -639,10 +657,11 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
         if (hipError_t err = ensure_dynamic_lds(fn, (int)kSkinnyDynLdsMax, lds_set[exact]); err != hipSuccess)
             return err;
         if (exact)
-            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true, SB, ONE>), dim3(grid), dim3(W * 64), lds, s, g);
+            hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, true, true, SB, ONE>), dim3(grid), dim3(W * 64), lds, s,
+                               LCML_SKINNY_LEAD(g, g.x, g.ldx), g);
         else
             hipLaunchKernelGGL((k_gemm_skinny<NB, 1, W, U, false, true, SB, ONE>), dim3(grid), dim3(W * 64), lds, s,
-                               g);
+                               LCML_SKINNY_LEAD(g, g.x, g.ldx), g);
         return hipGetLastError();
     };
     auto run = [&](auto sb) -> hipError_t {
