@@ -7,9 +7,10 @@ tree).  Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                             no v_pk_{add,mul,fma}_f32 generation
   -fvisibility=hidden                       only the LCML_API C symbols export
-  -mllvm -amdgpu-kernarg-preload-count=N    (gemm_skinny.hip, quantize.hip) the
-                                            N leading scalar kernel arguments
-                                            arrive in SGPRs at wave start
+  -mllvm -amdgpu-kernarg-preload-count=N    (gemm_skinny.hip, quantize.hip,
+                                            gemv_valu.hip) the N leading scalar
+                                            kernel arguments arrive in SGPRs
+                                            at wave start
 Usage:  python -m luisaml_amd.build   (or luisaml_amd.build.build())
 """
 from __future__ import annotations
@@ -44,6 +45,7 @@ COMMON = [
 EXTRA = {
     "gemm_skinny.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "quantize.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
+    "gemv_valu.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"],
 }
 
 

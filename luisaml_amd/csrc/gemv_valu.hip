@@ -50,63 +50,71 @@ __device__ inline void decode16(u4 w, float *f) {
     }
 }
 
-// 16 uniform activation values of row m, k-chunk c (zero beyond K).
+// 16 uniform activation values of row m, k-chunk c (zero beyond K) of the
+// activations act, row stride lda elements.
 template <bool FP8>
-__device__ inline void load_act16(const ValuArgs &g, int64_t m, int64_t c, float *a) {
+__device__ inline void load_act16(const void *act, int64_t lda, int K, int64_t m, int64_t c, float *a) {
     const int64_t k0 = c * 16;
     if (FP8) {
-        const uint8_t *row = static_cast<const uint8_t *>(g.a) + m * g.lda;
-        if (k0 + 16 <= g.K) {
+        const uint8_t *row = static_cast<const uint8_t *>(act) + m * lda;
+        if (k0 + 16 <= K) {
             cu32 *p = (cu32 *)(uintptr_t)(row + k0);
             u4 w = {p[0], p[1], p[2], p[3]};
             decode16(w, a);
         } else {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                f2 v = __builtin_amdgcn_cvt_pk_f32_fp8(k0 + j < g.K ? (int)row[k0 + j] : 0, false);
+                f2 v = __builtin_amdgcn_cvt_pk_f32_fp8(k0 + j < K ? (int)row[k0 + j] : 0, false);
                 a[j] = v.x;
             }
         }
     } else {
-        const float *row = static_cast<const float *>(g.a) + m * g.lda;
-        if (k0 + 16 <= g.K) {
+        const float *row = static_cast<const float *>(act) + m * lda;
+        if (k0 + 16 <= K) {
             cfloat *p = (cfloat *)(uintptr_t)(row + k0);
 #pragma unroll
             for (int j = 0; j < 16; ++j) a[j] = p[j];
         } else {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a[j] = k0 + j < g.K ? row[k0 + j] : 0.0f;
+            for (int j = 0; j < 16; ++j) a[j] = k0 + j < K ? row[k0 + j] : 0.0f;
         }
     }
 }
 
-// VMB rows per workgroup (1, 2 or 4; launch_valu chooses)
+// VMB rows per workgroup (1, 2 or 4; launch_valu chooses).  The values the
+// first loads depend on come as leading scalar arguments (the activations
+// and their row stride, the packed weights, M, K, the k-chunks per panel),
+// and this file is compiled with -amdgpu-kernarg-preload-count=6: they
+// arrive in SGPRs at wave start, so the first weight and activation loads
+// wait for no kernel-argument fetch.  The struct's copies are not read.
 template <bool FP8, int VMB>
-__global__ __launch_bounds__(kVW<FP8> * 64) void k_gemv_valu(ValuArgs g) {
+__global__ __launch_bounds__(kVW<FP8> * 64) void k_gemv_valu(const void *act, const uint8_t *bp, int64_t lda, int M,
+                                                              int K, int kc, ValuArgs g) {
     constexpr int VW = kVW<FP8>;
     static_assert(VMB <= VW, "one wavefront finalises one row");
     __shared__ float red[VW][VMB][64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t panel = blockIdx.x;
-    const int64_t m0 = (int64_t)blockIdx.y * VMB;
-    const int rows = (int)min((int64_t)VMB, g.M - m0);
-    const int64_t c_begin = (g.KC * wave) / VW, c_end = (g.KC * (wave + 1)) / VW;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int panel = blockIdx.x;
+    const int m0 = (int)blockIdx.y * VMB;
+    const int rows = min(VMB, M - m0);
+    // this wavefront's k-chunks (kc < 2^27: unsigned, so the divisions are shifts)
+    const int c_begin = (int)((uint32_t)(kc * wave) / VW), c_end = (int)((uint32_t)(kc * (wave + 1)) / VW);
     // chunks wholly beyond K hold zero weights; skip them
-    const int64_t c_live = (g.K + 15) / 16;
-    const int64_t c_stop = c_end < c_live ? c_end : c_live;
+    const int c_live = (K + 15) / 16;
+    const int c_stop = c_end < c_live ? c_end : c_live;
 
-    const uint8_t *wp = g.bp + panel * g.KC * 1024 + lane * 16;
+    const uint8_t *wp = bp + (size_t)panel * (size_t)kc * 1024 + lane * 16;
     float acc[VMB];
 #pragma unroll
     for (int r = 0; r < VMB; ++r) acc[r] = 0.0f;
 
     constexpr int U = 4;
-    for (int64_t c0 = c_begin; c0 < c_stop; c0 += U) {
+    for (int c0 = c_begin; c0 < c_stop; c0 += U) {
         u4 w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
             w[u] = c0 + u < c_stop
-                       ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(wp + (c0 + u) * 1024))
+                       ? __builtin_nontemporal_load(reinterpret_cast<const u4 *>(wp + (size_t)(c0 + u) * 1024))
                        : u4{0, 0, 0, 0};
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -117,7 +125,7 @@ __global__ __launch_bounds__(kVW<FP8> * 64) void k_gemv_valu(ValuArgs g) {
             for (int r = 0; r < VMB; ++r) {
                 if (r >= rows) break;
                 float a[16];
-                load_act16<FP8>(g, m0 + r, c0 + u, a);
+                load_act16<FP8>(act, lda, K, m0 + r, c0 + u, a);
 #pragma unroll
                 for (int j = 0; j < 16; ++j) acc[r] = fmaf(a[j], wf[j], acc[r]);
             }
@@ -129,13 +137,13 @@ __global__ __launch_bounds__(kVW<FP8> * 64) void k_gemv_valu(ValuArgs g) {
 
     const Epilogue &e = g.e;
     const float a_s = e.a_scale ? e.a_scale[0] : 1.0f;
-    const int64_t col = panel * 64 + lane;
+    const int64_t col = (int64_t)panel * 64 + lane;
     // wave w < VMB finalises row w of the block
     if (wave < VMB && wave < rows && col < e.N) {
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < VW; ++w) v += red[w][wave][lane];
-        const int64_t row = m0 + wave;
+        const int64_t row = (int64_t)m0 + wave;
         epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
     }
 }
@@ -157,12 +165,14 @@ hipError_t launch_valu(int64_t M, int64_t N, int64_t K, const void *a, int64_t l
     constexpr int64_t kFill = 256;
     const int vmb = npanels * ((M + 3) / 4) >= kFill ? 4 : npanels * ((M + 1) / 2) >= kFill ? 2 : 1;
     dim3 grid((unsigned)npanels, (unsigned)((M + vmb - 1) / vmb));
+#define LCML_VALU_LEAD g.a, g.bp, g.lda, (int)g.M, (int)g.K, (int)g.KC, g
     if (vmb == 4)
-        hipLaunchKernelGGL((k_gemv_valu<FP8, 4>), grid, dim3(kVW<FP8> * 64), 0, s, g);
+        hipLaunchKernelGGL((k_gemv_valu<FP8, 4>), grid, dim3(kVW<FP8> * 64), 0, s, LCML_VALU_LEAD);
     else if (vmb == 2)
-        hipLaunchKernelGGL((k_gemv_valu<FP8, 2>), grid, dim3(kVW<FP8> * 64), 0, s, g);
+        hipLaunchKernelGGL((k_gemv_valu<FP8, 2>), grid, dim3(kVW<FP8> * 64), 0, s, LCML_VALU_LEAD);
     else
-        hipLaunchKernelGGL((k_gemv_valu<FP8, 1>), grid, dim3(kVW<FP8> * 64), 0, s, g);
+        hipLaunchKernelGGL((k_gemv_valu<FP8, 1>), grid, dim3(kVW<FP8> * 64), 0, s, LCML_VALU_LEAD);
+#undef LCML_VALU_LEAD
     return hipGetLastError();
 }
 
