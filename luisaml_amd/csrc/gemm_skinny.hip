@@ -615,6 +615,9 @@ int skinny_row_blocks(int64_t M, int64_t N, int64_t K, double *cost) {
 
 hipError_t launch_gemm_skinny(int64_t M, int64_t N, int64_t K, const uint8_t *a, int64_t lda,
                               const uint8_t *bp, const Epilogue &e, bool exact, hipStream_t s) {
+    // 32-bit buffer extents and kernel arguments (the C ABI checks the same)
+    if ((M - 1) * lda + K >= ((int64_t)1 << 31) || pad_to(K, kPackK) * 64 >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;
     SkinnyArgs g;
     g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
     int64_t Kp = pad_to(K, kPackK), Np = pad_to(N, kPanelCols);
@@ -652,6 +655,9 @@ int64_t skinny_dynamic_lds_bytes(int64_t M, int64_t K) { return M * (pad_to(K, k
 hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const float *x, int64_t ldx,
                                       const uint8_t *bp, const Epilogue &e, float *scale_out, bool exact,
                                       hipStream_t s) {
+    // 32-bit buffer extents and kernel arguments (the C ABI checks the same)
+    if (((M - 1) * ldx + K) * 4 >= ((int64_t)1 << 31) || pad_to(K, kPackK) * 64 >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;
     SkinnyArgs g;
     g.M = M; g.N = N; g.K = K; g.a = nullptr; g.lda = 0; g.bp = bp;
     g.x = x; g.ldx = ldx; g.scale_out = scale_out;

@@ -151,6 +151,8 @@ __global__ __launch_bounds__(kVW<FP8> * 64) void k_gemv_valu(const void *act, co
 template <bool FP8>
 hipError_t launch_valu(int64_t M, int64_t N, int64_t K, const void *a, int64_t lda, const uint8_t *bp,
                        const Epilogue &e, hipStream_t s) {
+    // the kernel's leading arguments M, K and the k-chunks are 32-bit
+    if (M >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 31) - kPackK) return hipErrorInvalidValue;
     ValuArgs g;
     g.M = M; g.N = N; g.K = K; g.a = a; g.lda = lda; g.bp = bp;
     g.KC = pad_to(K, kPackK) / 16;
