@@ -34,9 +34,9 @@
 // at a time, right after issuing that block's weight loads: the ~40 VALU
 // operations per float4 of the exact encode run while the weights are in
 // flight, and only the first block's encode delays the stream.  When a
-// wavefront's blocks fit its 8 activation slots (ONE), the amax pass already
-// loads x in the per-block layout and the encode reuses those registers, so
-// x is read once.  (Encoding all of x before the main loop cost 1.55 us at
+// wavefront's blocks fit its 4 or 8 activation slots (ONE), the amax pass
+// already loads x in the per-block layout and the encode reuses those
+// registers, so x is read once.  (Encoding all of x before the main loop cost 1.55 us at
 // M=1 and 2.6 us at M=4 over the E4M3-in kernel on the 4096x11008 linear;
 // per block with one read of x, 0.6 and 1.0 us.)  The redundant
 // per-workgroup amax and encode still cost M*K loads and VALU work in every
@@ -99,8 +99,10 @@ __device__ inline v8i join(u4 lo, u4 hi) {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // SB (DYN only): activation slots of 4 floats per lane per K block, at least
-// ceil(M/2).  ONE (DYN only): every wavefront's K blocks fit 8 slots, so one
-// round of activation loads serves both the amax and the encode.
+// ceil(M/2).  ONE (DYN only; 0, 4 or 8): nonzero when every wavefront's K
+// blocks fit ONE slots, so that one round of ONE activation loads serves
+// both the amax and the encode (4 where they fit: at M <= 2 and K <= 4096
+// the four empty slots of an 8-slot round cost 0.1 us per launch).
 // The values that the code before the first weight load reads come as
 // leading scalar arguments (bp, the activations a or x with their row
 // stride, M, K, the panel's k-chunks, the K blocks, the row groups), and
@@ -110,7 +112,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // 4096x11008 linear the preload alone saved 0.05-0.15 us per launch, and
 // with the 32-bit prologue below (one weight offset per lane, the blocks'
 // pieces as immediate offsets) 0.26-0.39 us.
-template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0, bool ONE = false>
+template <int NB, int MB, int WAVES, int UNROLL, bool EXACT, bool DYN, int SB = 0, int ONE = 0>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, const void *src, int ld, int M, int K,
                                                             int kc, int nkb, int rg, SkinnyArgs g) {
     static_assert(!DYN || MB == 1, "the fused quantiser serves M <= 16");
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
     // memory round trip per UQ * 512 groups.  The first round is issued ahead
     // of the weight prefetch so that it returns from L2 without queueing
     // behind the HBM loads.
-    constexpr int UQ = 8;
+    constexpr int UQ = ONE ? ONE : 8;
     const uint32_t kq = (uint32_t)(K / 4);
     const uint32_t nq = (uint32_t)M * kq;
     const __amdgpu_buffer_rsrc_t x_rsrc =
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
         }
     };
     f4 v[UQ];
-    static_assert(!ONE || (DYN && UQ % SB == 0), "one round: whole blocks of slots");
+    static_assert(!ONE || (DYN && (ONE == 4 || ONE == 8) && UQ % SB == 0), "one round: whole blocks of slots");
     if constexpr (ONE) {
         // slot u holds slot u%SB of block kb_begin + u/SB (the per-block
         // layout above): the amax reads these registers, and the encode
@@ -671,11 +673,11 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
     const unsigned grid = (unsigned)((g.nblk16 + NB - 1) / NB);
     const unsigned lds = (unsigned)skinny_dynamic_lds_bytes(M, K);
     // activation slots per lane per K block: ceil(M/2), rounded up to 1, 2,
-    // 4, 8; one round of activation loads when a wavefront's K blocks (at
-    // most ceil(nkb / W)) take at most 8 slots
+    // 4, 8; one round of 4 or 8 activation loads when a wavefront's K blocks
+    // (at most ceil(nkb / W)) take at most that many slots
     auto run_one = [&](auto sb, auto one) -> hipError_t {
         constexpr int SB = decltype(sb)::value;
-        constexpr bool ONE = decltype(one)::value;
+        constexpr int ONE = decltype(one)::value;
         const void *fn = exact ? reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, true, true, SB, ONE>)
                                : reinterpret_cast<const void *>(k_gemm_skinny<NB, 1, W, U, false, true, SB, ONE>);
         static std::atomic<uint64_t> lds_set[2];
@@ -690,8 +692,12 @@ hipError_t launch_gemm_skinny_dynamic(int64_t M, int64_t N, int64_t K, const flo
         return hipGetLastError();
     };
     auto run = [&](auto sb) -> hipError_t {
-        if (((g.nkb + W - 1) / W) * decltype(sb)::value <= 8) return run_one(sb, std::true_type{});
-        return run_one(sb, std::false_type{});
+        constexpr int SB = decltype(sb)::value;
+        const int slots = ((g.nkb + W - 1) / W) * SB;
+        if constexpr (SB <= 4)
+            if (slots <= 4) return run_one(sb, std::integral_constant<int, 4>{});
+        if (slots <= 8) return run_one(sb, std::integral_constant<int, 8>{});
+        return run_one(sb, std::integral_constant<int, 0>{});
     };
     if (M <= 2) return run(std::integral_constant<int, 1>{});
     if (M <= 4) return run(std::integral_constant<int, 2>{});
