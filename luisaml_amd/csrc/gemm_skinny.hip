@@ -120,7 +120,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
     static_assert(!DYN || (SB >= 1 && SB <= 8 && LCML_SKINNY_PF == 1 && UNROLL == 1),
                   "the fused quantiser: M <= 2*SB <= 16, one K block per load");
     constexpr int NT = WAVES * 64;
-    __shared__ v4f red[WAVES][NB][64];
+    // the wavefronts' partial tiles, register r of lane l of block j at
+    // [w][j][r][l]: the epilogue's lanes read consecutive words (no bank
+    // conflicts; a [w][j][l] array of 16-byte partials had 4-way ones)
+    __shared__ float red[WAVES][NB][4][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // DYN: [M][pitch] E4M3
     // the wavefront index is uniform: readfirstlane lets the compiler keep
     // everything derived from it (the K range, the in-range tests) scalar
@@ -536,7 +539,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
     for (int mb = 0; mb < MB; ++mb) {
         if (mb) __syncthreads();  // the previous block's sums are read
 #pragma unroll
-        for (int j = 0; j < NB; ++j) red[wave][j][lane] = acc[mb][j];
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[mb][j][r];
         __syncthreads();
         if constexpr (MB == 1) {
             // Without C, alpha or an activation (a uniform test) the value is
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
                     if (o >= NB * 256 || row >= e.M || col >= e.N) continue;
                     float v = 0.0f;
 #pragma unroll
-                    for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
+                    for (int w = 0; w < WAVES; ++w) v += red[w][j][r][l];
                     if constexpr (decltype(pl)::value)
                         epi_store(e, row, col, v * (a_s * bsc[i]));
                     else
@@ -574,7 +579,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_skinny(const uint8_t *bp, c
                 if (row >= e.M || col >= e.N) continue;
                 float v = 0.0f;
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) v += red[w][j][l][r];
+                for (int w = 0; w < WAVES; ++w) v += red[w][j][r][l];
                 epi_store(e, row, col, epi_value(e, epi_scale(e, a_s, col), row, col, v));
             }
         }
